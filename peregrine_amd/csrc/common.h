@@ -1,0 +1,176 @@
+// common.h — shared device helpers and launch structures of libperegrine_hip.
+//
+// Arithmetic contract (identical to oracle/oracle.c, which restates
+// peregrine-kernels): every per-block integer dot is exact; every fp32
+// epilogue is evaluated in the same order with the same roundings. The whole
+// library is compiled with -ffp-contract=off so a*b+c never silently fuses.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace phip {
+
+// ---- activation scale granularity ("act group") ----
+// ACT_ROW: one scale per row (qrow_i8, peregrine-kernels/src/quant.rs:14-33).
+// ACT_B32: one scale per 32-element block (BASELINE extension).
+enum ActMode { ACT_ROW = 0, ACT_B32 = 1 };
+
+// ---- epilogue kinds (how int32 block dots become f32) ----
+//  EPI_ROW   per-row weight scale: D = sum of all block dots (exact int),
+//            y = ((f32)D * sc) * sx                   (matmul.rs:61-87)
+//  EPI_GRP   grouped weight scale, row act scale:
+//            acc = acc + sw[g]*(f32)d_g ; y = acc*sx   (matmul.rs:93-106)
+//  EPI_B32   32-block act scale (any weight grouping):
+//            acc = fmaf(sw(b)*sx[b], (f32)d_b, acc)   (BASELINE extension)
+enum Epi { EPI_ROW = 0, EPI_GRP = 1, EPI_B32 = 2 };
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 128-/64-bit streaming loads (weights are read once per dispatch).
+__device__ __forceinline__ uint4 ldg_stream4(const void *p) {
+    const u32x4 v = __builtin_nontemporal_load((const u32x4 *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ldg_stream2(const void *p) {
+    const u32x2 v = __builtin_nontemporal_load((const u32x2 *)p);
+    return make_uint2(v.x, v.y);
+}
+
+constexpr int TILE_O = 64;     // rows of a weight tile in the device layout
+constexpr int BLK = 32;        // K elements per block (one MFMA K step)
+
+// One expert's three resident tensors as the kernels see them.
+// Weights are tiled [Op/64][nb][64][BB] (BB = 16 bytes int4, 32 bytes int8);
+// scales are tiled [Op/64][ng][64] f32.
+struct ExpertDesc {
+    const uint8_t *w[3];   // gate, up, down
+    const float *sc[3];
+};
+
+// Per-matrix geometry shared by every expert of a call.
+struct MatGeom {
+    int K, Kp, nb;         // inputs, inputs padded to 32, blocks
+    int O, Op;             // outputs, outputs padded to 64
+    int gpb, ng;           // blocks per weight group, groups (per-row: gpb = nb, ng = 1)
+    int w4;                // 1: int4 weights, 0: int8
+    int per_row;           // weight scale per row
+};
+
+// Row bookkeeping of one MoE dispatch (device arrays).
+struct RowPlan {
+    const int *row_exp;    // [R] descriptor index of row r
+    const int *row_act;    // [R] activation row of row r
+    const int *mt_exp;     // [T] M-tile -> descriptor index
+    const int *mt_row0;    // [T] first row of the tile
+    const int *mt_rend;    // [T] one past the last row of that expert
+    const int *counts;     // [2] {R, T} as built on the device (or host)
+};
+
+// ---- device helpers ----
+
+// exp rounded once to f32 from a double-precision exp; equal to the correctly
+// rounded expf except within ~2^-28 of a midpoint. The oracle does the same.
+__device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x); }
+
+// siluf(x) * u — peregrine-model/src/math.rs:108-118 (division correctly rounded).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    float den = __fadd_rn(1.0f, exp_cr(-g));
+    return __fmul_rn(__fdiv_rn(g, den), u);
+}
+
+// Byte position of element k inside its 8-element group in the device
+// activation layout: even elements first, then odd (0,2,4,6,1,3,5,7). This is
+// the order the int4 unpack below produces from QT nibble pairs.
+__device__ __forceinline__ int perm8(int k) { return (k & ~7) | ((k & 1) << 2) | ((k & 7) >> 1); }
+
+// int4 QT dword (two's-complement nibbles after the upload XOR) -> two dwords
+// of int8 values scaled by 16: even elements and odd elements.
+__device__ __forceinline__ int i4_even16(uint32_t w) { return (int)((w << 4) & 0xF0F0F0F0u); }
+__device__ __forceinline__ int i4_odd16(uint32_t w) { return (int)(w & 0xF0F0F0F0u); }
+
+__device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// 32-block dot, int4 weights: 16 bytes of weights against 8 dwords of the
+// permuted activation block. Returns 16 * the exact dot.
+__device__ __forceinline__ int dot_blk_w4(uint4 w, const int *x) {
+    int acc = 0;
+    acc = sdot4(i4_even16(w.x), x[0], acc);
+    acc = sdot4(i4_odd16(w.x), x[1], acc);
+    acc = sdot4(i4_even16(w.y), x[2], acc);
+    acc = sdot4(i4_odd16(w.y), x[3], acc);
+    acc = sdot4(i4_even16(w.z), x[4], acc);
+    acc = sdot4(i4_odd16(w.z), x[5], acc);
+    acc = sdot4(i4_even16(w.w), x[6], acc);
+    acc = sdot4(i4_odd16(w.w), x[7], acc);
+    return acc;
+}
+
+// 32-block dot, int8 weights already in the permuted order. Exact dot.
+__device__ __forceinline__ int dot_blk_w8(uint4 a, uint4 b, const int *x) {
+    int acc = 0;
+    acc = sdot4((int)a.x, x[0], acc);
+    acc = sdot4((int)a.y, x[1], acc);
+    acc = sdot4((int)a.z, x[2], acc);
+    acc = sdot4((int)a.w, x[3], acc);
+    acc = sdot4((int)b.x, x[4], acc);
+    acc = sdot4((int)b.y, x[5], acc);
+    acc = sdot4((int)b.z, x[6], acc);
+    acc = sdot4((int)b.w, x[7], acc);
+    return acc;
+}
+
+template <typename T>
+__device__ __forceinline__ T warp_max(T v, int width) {
+    for (int off = width >> 1; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, width));
+    return v;
+}
+
+}  // namespace phip
+
+// ---- host-side launchers (defined in the kernel translation units) ----
+namespace phip {
+struct QuantArgs {
+    const float *x; int x_stride; int rows; int K; int Kp;
+    int8_t *q; int q_stride; float *s; int s_stride; int mode;
+};
+void launch_quant_rows(const QuantArgs &a, hipStream_t st);
+
+void launch_repack(const uint8_t *raw, const float *raw_sc, int fmt, int I, int O, int gs, uint8_t *w, float *sc,
+                   const MatGeom &g, hipStream_t st);
+
+struct DotArgs {   // shared by the GEMV and MFMA arms
+    const ExpertDesc *desc;
+    RowPlan plan;
+    const int8_t *xq; int x_stride; const float *sx; int sx_stride;   // activations
+    float *out; int out_stride;                                         // h (gate/up) or y (down)
+    int8_t *hq; int hq_stride; float *sh; int sh_stride;                // fused h quant (ACT_B32)
+    int32_t *dots;                                                      // optional per-block dot dump
+    int act_identity;                                                   // activation row = r (down proj)
+};
+// grid_rows / grid_tiles: host-side upper bounds; the kernels read the true
+// counts from plan.counts and idle the excess workgroups.
+void launch_gemv_gateup(const DotArgs &a, const MatGeom &g, int act, int grid_rows, hipStream_t st);
+void launch_gemv_down(const DotArgs &a, const MatGeom &g, int act, int grid_rows, hipStream_t st);
+void launch_mfma_gateup(const DotArgs &a, const MatGeom &g, int act, int grid_tiles, hipStream_t st);
+void launch_mfma_down(const DotArgs &a, const MatGeom &g, int act, int grid_tiles, hipStream_t st);
+
+void launch_combine(float *out, const float *y, const int *row_ptr, const int *row_idx, const float *rw,
+                    int s_n, int D, int y_stride, hipStream_t st);
+void launch_combine_padded(float *out, const float *y, const int *tok_rows, const float *rw, int s_n, int k, int D,
+                           int y_stride, hipStream_t st);
+void launch_route_softmax(const float *logits, int S, int E, int k, int *ids, float *w, hipStream_t st);
+
+struct TableOut {
+    int *hdr;          // [4]: R, T, n_u, flags
+    int *uexp, *off;   // [E], [E+1]
+    int *row_tok, *row_kk, *row_exp;  // [R]
+    int *tok_ptr, *tok_rows;          // [S+1], [S*k] (CSR of each token's rows, union order)
+    float *rw_row;     // [R]
+    int *mt_exp, *mt_row0, *mt_rend;  // [Tmax]
+};
+void launch_synth_fill(void *dst, size_t n, int kind, float a, float b, uint64_t seed, hipStream_t st);
+void launch_build_table(const int *ids, const float *w, int S, int k, int E, const TableOut &t, int tmax,
+                        hipStream_t st);
+}  // namespace phip

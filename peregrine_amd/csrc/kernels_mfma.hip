@@ -1,0 +1,252 @@
+// kernels_mfma.hip — the batched arm: per-expert grouped GEMM on the int8
+// matrix cores (v_mfma_i32_32x32x32_i8, gfx950).
+//
+// Work unit: one 32-row M-tile of one expert (from the expert-offset table)
+// times a slab of output channels. One MFMA consumes exactly one 32-element
+// K block, so each block's int32 dot leaves the matrix core whole and the f32
+// epilogue runs block by block in ascending order — the same chain as
+// oracle/oracle.c, element for element. With a per-row weight scale (or a
+// group spanning several blocks) the int32 dots accumulate inside the MFMA
+// and the f32 step runs once per group.
+//
+// Operand mapping (A = activations, rows = tokens; B = weights, columns =
+// output channels): lane l supplies row/column (l % 32) and the K half
+// (l / 32); A and B use the same K slots, so the integer dot is the exact
+// sum whatever order the hardware walks K in. Accumulator register r of
+// lane l holds row 8*(r/4) + 4*(l/32) + r%4, column l % 32.
+//
+// int4 weights are unpacked in registers: 8 bytes (16 nibbles) per lane per
+// block -> 16 int8 values scaled by 16 (the scale tables carry the 1/16).
+#include "common.h"
+
+namespace phip {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+template <bool W4>
+__device__ __forceinline__ v4i load_b(const uint8_t *p) {
+    v4i r;
+    if constexpr (W4) {
+        const uint2 w = ldg_stream2(p);
+        r[0] = i4_even16(w.x);
+        r[1] = i4_odd16(w.x);
+        r[2] = i4_even16(w.y);
+        r[3] = i4_odd16(w.y);
+    } else {
+        const uint4 w = ldg_stream4(p);
+        r[0] = (int)w.x;
+        r[1] = (int)w.y;
+        r[2] = (int)w.z;
+        r[3] = (int)w.w;
+    }
+    return r;
+}
+
+__device__ __forceinline__ int acc_row(int reg, int lane) { return 8 * (reg >> 2) + 4 * (lane >> 5) + (reg & 3); }
+
+// NSUB column subtiles of 32 per wave. GATEUP: subtile 0 = gate, 1 = up (same
+// channels). Down: NSUB adjacent 32-channel subtiles.
+template <bool W4, int EPI, bool GATEUP, int NSUB>
+__global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const int8_t *__restrict__ xq,
+                                                   const float *__restrict__ sxv) {
+    constexpr int BB = W4 ? 16 : 32;
+    extern __shared__ float sxl[];   // EPI_B32: [nb][32] activation scales of this tile's rows
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tile = blockIdx.y;
+    if (tile >= a.plan.counts[1]) return;
+    const int e = a.plan.mt_exp[tile], r0 = a.plan.mt_row0[tile], rend = a.plan.mt_rend[tile];
+    const int j = lane & 31, hh = lane >> 5;
+    const int n0 = GATEUP ? ((int)blockIdx.x * 4 + wave) * 32 : ((int)blockIdx.x * 4 + wave) * 32 * NSUB;
+
+    // activation row of this lane's A slot (rows past the expert's end repeat
+    // its last row; their results are never stored)
+    int ra = r0 + j;
+    if (ra >= rend) ra = rend - 1;
+    const int arow_a = a.act_identity ? ra : a.plan.row_act[ra];
+    const int8_t *xa = xq + (size_t)arow_a * a.x_stride + hh * 16;
+
+    if constexpr (EPI == EPI_B32) {
+        for (int idx = threadIdx.x; idx < 32 * g.nb; idx += 256) {
+            const int i = idx & 31, b = idx >> 5;
+            int rr = r0 + i;
+            if (rr >= rend) rr = rend - 1;
+            const int ar = a.act_identity ? rr : a.plan.row_act[rr];
+            sxl[b * 32 + i] = sxv[(size_t)ar * a.sx_stride + b];
+        }
+        __syncthreads();
+    }
+
+    const uint8_t *wp[NSUB];
+    const float *sp[NSUB];
+    int oc[NSUB];
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) {
+        const int mat = GATEUP ? s : 2;
+        int o = GATEUP ? n0 + j : n0 + s * 32 + j;
+        oc[s] = o;
+        if (o >= g.Op) o = g.Op - 1;
+        wp[s] = a.desc[e].w[mat] + ((size_t)(o >> 6) * g.nb * TILE_O + (o & 63)) * BB + hh * (BB / 2);
+        sp[s] = a.desc[e].sc[mat] + (size_t)(o >> 6) * g.ng * TILE_O + (o & 63);
+    }
+
+    float acc[NSUB][16];
+    v16i iacc[NSUB];
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[s][i] = 0.0f;
+        iacc[s] = v16i{};
+    }
+
+    // software pipeline: operands of block b+1 load while block b computes
+    v4i A = *(const v4i *)xa;
+    v4i B[NSUB];
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) B[s] = load_b<W4>(wp[s]);
+
+    for (int b = 0; b < g.nb; ++b) {
+        v4i An = A, Bn[NSUB];
+        const int bn = b + 1 < g.nb ? b + 1 : b;
+        An = *(const v4i *)(xa + (size_t)bn * BLK);
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) Bn[s] = load_b<W4>(wp[s] + (size_t)bn * TILE_O * BB);
+
+        const bool gend = ((b + 1) % g.gpb == 0) || (b + 1 == g.nb);
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) {
+            const v16i cin = (EPI == EPI_B32) ? v16i{} : iacc[s];
+            const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B[s], cin, 0, 0, 0);
+            if (a.dots) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int row = r0 + acc_row(i, lane);
+                    const int val = d[i] - (EPI == EPI_B32 ? 0 : cin[i]);
+                    if (row < rend && oc[s] < g.O)
+                        a.dots[(((size_t)row * (GATEUP ? 2 : 1) + (GATEUP ? s : 0)) * g.O + oc[s]) * g.nb + b] =
+                            W4 ? (val >> 4) : val;
+                }
+            }
+            if constexpr (EPI == EPI_ROW) {
+                iacc[s] = d;
+            } else if constexpr (EPI == EPI_GRP) {
+                if (gend) {
+                    const float sw = sp[s][(size_t)(b / g.gpb) * TILE_O];
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) acc[s][i] = __fadd_rn(acc[s][i], __fmul_rn((float)d[i], sw));
+                    iacc[s] = v16i{};
+                } else {
+                    iacc[s] = d;
+                }
+            } else {
+                const float sw = sp[s][(size_t)(b / g.gpb) * TILE_O];
+                const float4 *sx4 = (const float4 *)(sxl + b * 32 + 4 * hh);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 sq = sx4[2 * q];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const float sxr = t == 0 ? sq.x : t == 1 ? sq.y : t == 2 ? sq.z : sq.w;
+                        const int i = 4 * q + t;
+                        acc[s][i] = __fmaf_rn(__fmul_rn(sw, sxr), (float)d[i], acc[s][i]);
+                    }
+                }
+            }
+        }
+        A = An;
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) B[s] = Bn[s];
+    }
+
+    // per-row activation scale (EPI_ROW / EPI_GRP) of each accumulator row
+    float v[NSUB][16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        float sxr = 1.0f;
+        if constexpr (EPI != EPI_B32) {
+            int rr = r0 + acc_row(i, lane);
+            if (rr >= rend) rr = rend - 1;
+            const int ar = a.act_identity ? rr : a.plan.row_act[rr];
+            sxr = sxv[(size_t)ar * a.sx_stride];
+        }
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) {
+            if constexpr (EPI == EPI_ROW) {
+                const int D = W4 ? (iacc[s][i] >> 4) : iacc[s][i];
+                const float sc = W4 ? __fmul_rn(sp[s][0], 16.0f) : sp[s][0];
+                v[s][i] = __fmul_rn(__fmul_rn((float)D, sc), sxr);
+            } else if constexpr (EPI == EPI_GRP) {
+                v[s][i] = __fmul_rn(acc[s][i], sxr);
+            } else {
+                v[s][i] = acc[s][i];
+            }
+        }
+    }
+
+    if constexpr (GATEUP) {
+        const int o = oc[0];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int row = r0 + acc_row(i, lane);
+            const float h = silu_mul(v[0][i], v[1][i]);
+            const bool ok = row < rend && o < ((g.O + 31) & ~31);
+            if (ok) a.out[(size_t)row * a.out_stride + o] = h;
+            if (EPI == EPI_B32 && a.hq) {
+                // one h row's 32 channels live in the 32 lanes of this half-wave
+                const float m = warp_max(fabsf(h), 32);
+                float sc = __fdiv_rn(m, 127.0f);
+                if (sc < 1e-12f) sc = 1e-12f;
+                const float inv = __fdiv_rn(1.0f, sc);
+                if (ok) {
+                    a.hq[(size_t)row * a.hq_stride + perm8(o)] = (int8_t)(int)rintf(__fmul_rn(h, inv));
+                    if (j == 0) a.sh[(size_t)row * a.sh_stride + (o >> 5)] = sc;
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) {
+            const int o = oc[s];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int row = r0 + acc_row(i, lane);
+                if (row < rend && o < g.O) a.out[(size_t)row * a.out_stride + o] = v[s][i];
+            }
+        }
+    }
+}
+
+template <bool W4, int EPI, bool GATEUP>
+static void launch_mfma_t(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
+    constexpr int NSUB = 2;
+    const int ch_per_wg = GATEUP ? 4 * 32 : 4 * 32 * NSUB;
+    const int span = GATEUP ? ((g.O + 31) & ~31) : g.O;
+    dim3 grid((unsigned)((span + ch_per_wg - 1) / ch_per_wg), (unsigned)grid_tiles);
+    const size_t lds = EPI == EPI_B32 ? (size_t)g.nb * 32 * sizeof(float) : 0;
+    hipLaunchKernelGGL((mfma_kernel<W4, EPI, GATEUP, NSUB>), grid, dim3(256), lds, st, a, g, a.xq, a.sx);
+}
+
+template <bool GATEUP>
+static void launch_mfma_any(const DotArgs &a, const MatGeom &g, int act, int grid_tiles, hipStream_t st) {
+    if (grid_tiles <= 0) return;
+    const int epi = act == ACT_B32 ? EPI_B32 : (g.per_row ? EPI_ROW : EPI_GRP);
+    if (g.w4) {
+        if (epi == EPI_ROW) launch_mfma_t<true, EPI_ROW, GATEUP>(a, g, grid_tiles, st);
+        else if (epi == EPI_GRP) launch_mfma_t<true, EPI_GRP, GATEUP>(a, g, grid_tiles, st);
+        else launch_mfma_t<true, EPI_B32, GATEUP>(a, g, grid_tiles, st);
+    } else {
+        if (epi == EPI_ROW) launch_mfma_t<false, EPI_ROW, GATEUP>(a, g, grid_tiles, st);
+        else if (epi == EPI_GRP) launch_mfma_t<false, EPI_GRP, GATEUP>(a, g, grid_tiles, st);
+        else launch_mfma_t<false, EPI_B32, GATEUP>(a, g, grid_tiles, st);
+    }
+}
+
+void launch_mfma_gateup(const DotArgs &a, const MatGeom &g, int act, int grid_tiles, hipStream_t st) {
+    launch_mfma_any<true>(a, g, act, grid_tiles, st);
+}
+void launch_mfma_down(const DotArgs &a, const MatGeom &g, int act, int grid_tiles, hipStream_t st) {
+    launch_mfma_any<false>(a, g, act, grid_tiles, st);
+}
+
+}  // namespace phip

@@ -1,0 +1,991 @@
+// runtime.hip — the C ABI of libperegrine_hip.so: device contexts, resident
+// tensors, per-device scratch, the expert-group dispatch and the
+// device-resident MoE layer. Replaces cuda/backend_cuda.cu's host side
+// (contexts :484-592, tensors :747-810, expert_group_impl :1035-1243).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "../../include/peregrine_hip.h"
+#include "common.h"
+
+using namespace phip;
+
+struct ColiHipTensor {
+    int fmt, I, O, gs, device;
+    MatGeom g;
+    uint8_t *w;
+    float *sc;
+    size_t w_bytes, sc_bytes;
+};
+
+struct ColiHipGraph {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+    int device;
+};
+
+struct ColiHipExpertSet {
+    int device, count;
+    MatGeom gg, gd;          // gate/up geometry, down geometry
+    ExpertDesc *desc_dev;    // [count]
+};
+
+namespace {
+
+struct Buf {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+
+constexpr int GRAPH_CACHE = 16;
+constexpr int N_EVENTS = 2 * COLI_HIP_K_COUNT + 4;
+
+struct Ctx {
+    int device = -1;
+    hipStream_t stream = nullptr;
+    size_t tensor_count = 0, tensor_bytes = 0;
+    unsigned gen = 0;   // bumped on every scratch reallocation
+    Buf xq, sx, h, hq, sh, y, red_out, meta, tbl;
+    Buf pin_x, pin_y, pin_meta;
+    hipEvent_t ev[N_EVENTS] = {};
+    hipEvent_t user_ev[16] = {};
+    // last device-resident table (for coli_hip_last_table)
+    TableOut tbl_view{};
+    int tbl_E = 0, tbl_R = 0;
+};
+
+Ctx g_ctx[COLI_HIP_MAX_DEVICES];
+int g_nctx = 0;
+std::mutex g_stats_mu;
+uint64_t g_calls = 0, g_experts = 0, g_rows = 0;
+double g_h2d_ms = 0, g_kernel_ms = 0, g_d2h_ms = 0;
+uint64_t g_k_launches[COLI_HIP_K_COUNT] = {};
+double g_k_ms[COLI_HIP_K_COUNT] = {};
+uint64_t g_graph_captures = 0, g_graph_replays = 0, g_graph_invalidations = 0, g_graph_uncacheable = 0;
+int g_act_group = -1;   // -1: read COLI_HIP_ACT_GROUP on first use
+int g_arm = -2;         // -2: read COLI_HIP_ARM on first use
+int g_profile = -1;
+int32_t *g_dbg_gu = nullptr, *g_dbg_dn = nullptr;
+thread_local int g_cur_dev = -1;
+
+int hip_ok(hipError_t e, const char *what) {
+    if (e == hipSuccess) return 1;
+    std::fprintf(stderr, "[HIP] %s: %s\n", what, hipGetErrorString(e));
+    return 0;
+}
+
+int fail(const char *what) {
+    std::fprintf(stderr, "[HIP] %s\n", what);
+    return 0;
+}
+
+int env_int(const char *name, int dflt) {
+    const char *v = std::getenv(name);
+    return v && *v ? std::atoi(v) : dflt;
+}
+
+int act_group() {
+    if (g_act_group < 0) g_act_group = env_int("COLI_HIP_ACT_GROUP", 0) == 32 ? 32 : 0;
+    return g_act_group;
+}
+
+int forced_arm() {
+    if (g_arm == -2) {
+        const char *v = std::getenv("COLI_HIP_ARM");
+        g_arm = -1;
+        if (v && !std::strcmp(v, "gemv")) g_arm = COLI_HIP_ARM_GEMV;
+        if (v && !std::strcmp(v, "mfma")) g_arm = COLI_HIP_ARM_MFMA;
+    }
+    return g_arm;
+}
+
+int profiling() {
+    if (g_profile < 0) g_profile = env_int("COLI_HIP_PROFILE", 0) ? 1 : 0;
+    return g_profile;
+}
+
+Ctx *find_ctx(int device) {
+    for (int i = 0; i < g_nctx; i++)
+        if (g_ctx[i].device == device) return &g_ctx[i];
+    return nullptr;
+}
+
+int select_ctx(Ctx *c) {
+    if (!c) return 0;
+    if (g_cur_dev == c->device) return 1;
+    if (!hip_ok(hipSetDevice(c->device), "select device")) return 0;
+    g_cur_dev = c->device;
+    return 1;
+}
+
+// Grow-only device scratch. A reallocation bumps the generation so anything
+// holding baked addresses (captured graphs) knows it is stale.
+int reserve(Ctx *c, Buf &b, size_t bytes) {
+    if (bytes == 0) bytes = 256;
+    if (b.cap >= bytes) return 1;
+    if (b.p) hipFree(b.p);
+    b.p = nullptr;
+    b.cap = 0;
+    c->gen++;
+    if (!hip_ok(hipMalloc(&b.p, bytes), "scratch allocation")) return 0;
+    b.cap = bytes;
+    return 1;
+}
+
+int reserve_pinned(Ctx *c, Buf &b, size_t bytes) {
+    if (bytes == 0) bytes = 256;
+    if (b.cap >= bytes) return 1;
+    if (b.p) hipHostFree(b.p);
+    b.p = nullptr;
+    b.cap = 0;
+    c->gen++;
+    if (!hip_ok(hipHostMalloc(&b.p, bytes, hipHostMallocDefault), "pinned staging allocation")) return 0;
+    b.cap = bytes;
+    return 1;
+}
+
+void free_ctx(Ctx *c) {
+    Buf *dev[] = {&c->xq, &c->sx, &c->h, &c->hq, &c->sh, &c->y, &c->red_out, &c->meta, &c->tbl};
+    for (Buf *b : dev) {
+        if (b->p) hipFree(b->p);
+        *b = Buf{};
+    }
+    Buf *pin[] = {&c->pin_x, &c->pin_y, &c->pin_meta};
+    for (Buf *b : pin) {
+        if (b->p) hipHostFree(b->p);
+        *b = Buf{};
+    }
+    for (auto &e : c->ev)
+        if (e) {
+            hipEventDestroy(e);
+            e = nullptr;
+        }
+    for (auto &e : c->user_ev)
+        if (e) {
+            hipEventDestroy(e);
+            e = nullptr;
+        }
+    if (c->stream) hipStreamDestroy(c->stream);
+    c->stream = nullptr;
+}
+
+size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
+
+int make_geom(int fmt, int I, int O, int gs, MatGeom *g) {
+    const bool grouped = fmt == COLI_HIP_FMT_I4G || fmt == COLI_HIP_FMT_I8G;
+    if (I < 1 || O < 1) return fail("tensor shape must be positive");
+    if (!(fmt == COLI_HIP_FMT_I8 || fmt == COLI_HIP_FMT_I4 || grouped)) {
+        std::fprintf(stderr, "[HIP] weight format %d is not supported (1, 2, 4, 8)\n", fmt);
+        return 0;
+    }
+    if (grouped && gs != 32 && gs != 64 && gs != 128 && gs != 256) {
+        std::fprintf(stderr, "[HIP] group size %d is not supported (32, 64, 128, 256)\n", gs);
+        return 0;
+    }
+    g->K = I;
+    g->Kp = (int)round_up((size_t)I, 32);
+    g->nb = g->Kp / 32;
+    g->O = O;
+    g->Op = (int)round_up((size_t)O, 64);
+    g->w4 = (fmt == COLI_HIP_FMT_I4 || fmt == COLI_HIP_FMT_I4G) ? 1 : 0;
+    g->per_row = grouped ? 0 : 1;
+    g->gpb = grouped ? gs / 32 : g->nb;
+    g->ng = grouped ? (g->nb + g->gpb - 1) / g->gpb : 1;
+    return 1;
+}
+
+size_t raw_weight_bytes(int fmt, int I, int O) {
+    const bool w4 = fmt == COLI_HIP_FMT_I4 || fmt == COLI_HIP_FMT_I4G;
+    return (size_t)O * (w4 ? (size_t)(I + 1) / 2 : (size_t)I);
+}
+
+size_t raw_scale_count(const MatGeom &g) { return (size_t)g.O * g.ng; }
+
+void tensor_release(ColiHipTensor *t) {
+    if (!t) return;
+    if (t->w) hipFree(t->w);
+    if (t->sc) hipFree(t->sc);
+    std::free(t);
+}
+
+// Repack raw QT bytes/scales (device pointers) into t's tiled layout; blocks.
+int repack_into(Ctx *c, ColiHipTensor *t, const void *raw_w, const float *raw_sc) {
+    launch_repack((const uint8_t *)raw_w, raw_sc, t->fmt, t->I, t->O, t->gs, t->w, t->sc, t->g, c->stream);
+    return hip_ok(hipGetLastError(), "weight repack launch") &&
+           hip_ok(hipStreamSynchronize(c->stream), "weight repack");
+}
+
+// Copy host raw weights to a temporary device buffer, then repack.
+int repack_from_host(Ctx *c, ColiHipTensor *t, const void *w, const float *scales) {
+    const size_t wb = raw_weight_bytes(t->fmt, t->I, t->O), sb = raw_scale_count(t->g) * sizeof(float);
+    void *tmp = nullptr;
+    if (!hip_ok(hipMalloc(&tmp, round_up(wb, 256) + sb), "upload staging")) return 0;
+    int ok = hip_ok(hipMemcpy(tmp, w, wb, hipMemcpyHostToDevice), "tensor upload") &&
+             hip_ok(hipMemcpy((uint8_t *)tmp + round_up(wb, 256), scales, sb, hipMemcpyHostToDevice), "scale upload") &&
+             repack_into(c, t, tmp, (const float *)((uint8_t *)tmp + round_up(wb, 256)));
+    hipFree(tmp);
+    return ok;
+}
+
+int upload_impl(ColiHipTensor **tensor, const void *weights, const float *scales, int fmt, int I, int O, int gs,
+                int device, bool from_device) {
+    Ctx *c = find_ctx(device);
+    if (!tensor || !weights || !scales || !select_ctx(c)) return 0;
+    MatGeom g{};
+    if (!make_geom(fmt, I, O, gs, &g)) return 0;
+    const int gs_eff = g.per_row ? 0 : gs;
+    if (*tensor) {
+        const ColiHipTensor *t = *tensor;
+        return t->fmt == fmt && t->I == I && t->O == O && t->device == device && t->gs == gs_eff;
+    }
+    ColiHipTensor *t = (ColiHipTensor *)std::calloc(1, sizeof(ColiHipTensor));
+    if (!t) return 0;
+    t->fmt = fmt;
+    t->I = I;
+    t->O = O;
+    t->gs = gs_eff;
+    t->device = device;
+    t->g = g;
+    t->w_bytes = (size_t)g.Op * g.nb * (g.w4 ? 16 : 32);
+    t->sc_bytes = (size_t)g.Op * g.ng * sizeof(float);
+    if (!hip_ok(hipMalloc(&t->w, t->w_bytes), "tensor allocation") ||
+        !hip_ok(hipMalloc(&t->sc, t->sc_bytes), "scale allocation")) {
+        tensor_release(t);
+        return 0;
+    }
+    const int ok = from_device ? repack_into(c, t, weights, scales) : repack_from_host(c, t, weights, scales);
+    if (!ok) {
+        tensor_release(t);
+        return 0;
+    }
+    c->tensor_count++;
+    c->tensor_bytes += t->w_bytes + t->sc_bytes;
+    *tensor = t;
+    return 1;
+}
+
+int epi_act(int ga) { return ga == 32 ? ACT_B32 : ACT_ROW; }
+
+// Validate a gate/up/down triple list; fills the two geometries.
+int check_group(ColiHipTensor *const *gates, ColiHipTensor *const *ups, ColiHipTensor *const *downs, int count,
+                int *device, MatGeom *gg, MatGeom *gd) {
+    if (!gates || !ups || !downs || count < 1) return 0;
+    const ColiHipTensor *g0 = gates[0], *d0 = downs[0];
+    if (!g0 || !d0) return 0;
+    const int D = g0->I, I = g0->O;
+    for (int c = 0; c < count; c++) {
+        const ColiHipTensor *g = gates[c], *u = ups[c], *d = downs[c];
+        if (!g || !u || !d) return 0;
+        if (g->device != g0->device || u->device != g0->device || d->device != g0->device) return 0;
+        if (g->I != D || u->I != D || g->O != I || u->O != I || d->I != I || d->O != D) return 0;
+        if (g->fmt != g0->fmt || u->fmt != g0->fmt || g->gs != g0->gs || u->gs != g0->gs)
+            return fail("expert group: gate/up formats differ within the call");
+        if (d->fmt != d0->fmt || d->gs != d0->gs) return fail("expert group: down formats differ within the call");
+    }
+    *device = g0->device;
+    *gg = g0->g;
+    *gd = d0->g;
+    return 1;
+}
+
+void note_group(int count, int total) {
+    std::lock_guard<std::mutex> lock(g_stats_mu);
+    g_calls++;
+    g_experts += (uint64_t)count;
+    g_rows += (uint64_t)total;
+}
+
+// Records kernel-boundary events when profiling; accumulates at finish().
+struct Prof {
+    Ctx *c;
+    bool on;
+    int n = 0;
+    int which[N_EVENTS];
+    explicit Prof(Ctx *ctx) : c(ctx), on(profiling() != 0) {
+        if (!on) return;
+        for (auto &e : c->ev)
+            if (!e && hipEventCreate(&e) != hipSuccess) on = false;
+    }
+    void mark(int w) {   // event before kernel w (w = -1: final)
+        if (!on || n >= N_EVENTS) return;
+        which[n] = w;
+        hipEventRecord(c->ev[n++], c->stream);
+    }
+    void finish() {
+        if (!on || n < 2) return;
+        hipEventSynchronize(c->ev[n - 1]);
+        std::lock_guard<std::mutex> lock(g_stats_mu);
+        for (int i = 0; i + 1 < n; i++) {
+            float ms = 0;
+            if (which[i] < 0) continue;
+            hipEventElapsedTime(&ms, c->ev[i], c->ev[i + 1]);
+            g_k_launches[which[i]]++;
+            g_k_ms[which[i]] += ms;
+        }
+    }
+};
+
+struct Scratch {
+    int8_t *xq;
+    float *sx, *h;
+    int8_t *hq;
+    float *sh, *y;
+    int xs, sxs, hs, hqs, shs, ys;
+};
+
+// Reserve per-row scratch for `rows_x` activation rows and `R` expert rows.
+int reserve_rows(Ctx *c, const MatGeom &gg, const MatGeom &gd, int rows_x, int R, int ga, Scratch *s) {
+    s->xs = gg.Kp;
+    s->sxs = ga == 32 ? gg.nb : 1;
+    s->hs = gd.Kp;   // h row: I padded to 32 (= down's K layout)
+    s->hqs = gd.Kp;
+    s->shs = ga == 32 ? gd.nb : 1;
+    s->ys = gd.O;
+    if (!reserve(c, c->xq, (size_t)rows_x * s->xs) || !reserve(c, c->sx, (size_t)rows_x * s->sxs * 4) ||
+        !reserve(c, c->h, (size_t)R * s->hs * 4) || !reserve(c, c->hq, (size_t)R * s->hqs) ||
+        !reserve(c, c->sh, (size_t)R * s->shs * 4) || !reserve(c, c->y, (size_t)R * s->ys * 4))
+        return 0;
+    s->xq = (int8_t *)c->xq.p;
+    s->sx = (float *)c->sx.p;
+    s->h = (float *)c->h.p;
+    s->hq = (int8_t *)c->hq.p;
+    s->sh = (float *)c->sh.p;
+    s->y = (float *)c->y.p;
+    return 1;
+}
+
+// The kernel sequence of one dispatch after the activations are on the
+// device: quantise x, gate/up (+SwiGLU), [quantise h], down.
+void run_experts(Ctx *c, Prof &prof, const ExpertDesc *desc, const RowPlan &plan, const MatGeom &gg,
+                 const MatGeom &gd, const float *x_dev, int rows_x, bool x_identity, int R_bound, int T_bound,
+                 int ga, int arm, const Scratch &s) {
+    const int act = epi_act(ga);
+    QuantArgs qa{x_dev, gg.K, rows_x, gg.K, gg.Kp, s.xq, s.xs, s.sx, s.sxs, act};
+    prof.mark(COLI_HIP_K_QUANT_X);
+    launch_quant_rows(qa, c->stream);
+
+    DotArgs da{};
+    da.desc = desc;
+    da.plan = plan;
+    da.xq = s.xq;
+    da.x_stride = s.xs;
+    da.sx = s.sx;
+    da.sx_stride = s.sxs;
+    da.out = s.h;
+    da.out_stride = s.hs;
+    da.hq = act == ACT_B32 ? s.hq : nullptr;
+    da.hq_stride = s.hqs;
+    da.sh = s.sh;
+    da.sh_stride = s.shs;
+    da.dots = g_dbg_gu;
+    da.act_identity = x_identity ? 1 : 0;
+    prof.mark(COLI_HIP_K_GATEUP);
+    if (arm == COLI_HIP_ARM_GEMV)
+        launch_gemv_gateup(da, gg, act, R_bound, c->stream);
+    else
+        launch_mfma_gateup(da, gg, act, T_bound, c->stream);
+
+    if (act == ACT_ROW) {
+        QuantArgs qh{s.h, s.hs, R_bound, gd.K, gd.Kp, s.hq, s.hqs, s.sh, s.shs, ACT_ROW};
+        prof.mark(COLI_HIP_K_QUANT_H);
+        launch_quant_rows(qh, c->stream);
+    }
+
+    DotArgs dd = da;
+    dd.xq = s.hq;
+    dd.x_stride = s.hqs;
+    dd.sx = s.sh;
+    dd.sx_stride = s.shs;
+    dd.out = s.y;
+    dd.out_stride = s.ys;
+    dd.hq = nullptr;
+    dd.sh = nullptr;
+    dd.dots = g_dbg_dn;
+    dd.act_identity = 1;
+    prof.mark(COLI_HIP_K_DOWN);
+    if (arm == COLI_HIP_ARM_GEMV)
+        launch_gemv_down(dd, gd, act, R_bound, c->stream);
+    else
+        launch_mfma_down(dd, gd, act, T_bound, c->stream);
+}
+
+struct ReduceSpec {
+    const int *row_ptr, *row_idx;
+    const float *rw;
+    int s_n;
+    float *out;
+};
+
+int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, ColiHipTensor *const *downs,
+                      const int *rows, int count, float *y, const float *x, const ReduceSpec *red, int *arm_out) {
+    if (!rows || !x || count < 1) return 0;
+    if (!red && !y) return 0;
+    if (red && (!red->row_ptr || !red->row_idx || !red->rw || !red->out || red->s_n < 1)) return 0;
+    if (count > 256) return fail("expert group: more than 256 experts in one call");
+    int device = -1;
+    MatGeom gg{}, gd{};
+    if (!check_group(gates, ups, downs, count, &device, &gg, &gd)) return 0;
+    int total = 0, max_rows = 0;
+    for (int c = 0; c < count; c++) {
+        if (rows[c] < 1) return 0;
+        total += rows[c];
+        max_rows = std::max(max_rows, rows[c]);
+    }
+    if (red) {
+        if (red->row_ptr[0] != 0 || red->row_ptr[red->s_n] != total) return fail("reduce: row_ptr does not span rows");
+        for (int s = 0; s < red->s_n; s++)
+            if (red->row_ptr[s + 1] < red->row_ptr[s]) return fail("reduce: row_ptr not ascending");
+        for (int j = 0; j < total; j++)
+            if (red->row_idx[j] < 0 || red->row_idx[j] >= total) return fail("reduce: row_idx out of range");
+    }
+    Ctx *c = find_ctx(device);
+    if (!select_ctx(c)) return 0;
+    const int D = gg.K, ga = act_group();
+    int arm = forced_arm();
+    if (arm < 0) arm = max_rows <= 1 ? COLI_HIP_ARM_GEMV : COLI_HIP_ARM_MFMA;
+    if (arm_out) *arm_out = arm;
+
+    // host-built plan: descriptors in call order, rows consecutive
+    int T = 0;
+    for (int i = 0; i < count; i++) T += (rows[i] + 31) / 32;
+    const int s_n = red ? red->s_n : 0;
+    const size_t n_int = (size_t)total /*row_exp*/ + 3 * (size_t)T + 2 + (red ? (size_t)(s_n + 1) + total : 0);
+    const size_t desc_b = round_up((size_t)count * sizeof(ExpertDesc), 16);
+    const size_t meta_b = desc_b + n_int * 4 + (red ? (size_t)total * 4 : 0);
+    const size_t xb = (size_t)total * D * 4;
+    const size_t ob = red ? (size_t)s_n * D * 4 : xb;
+    Scratch s{};
+    if (!reserve_rows(c, gg, gd, total, total, ga, &s) || !reserve(c, c->meta, meta_b) ||
+        !reserve_pinned(c, c->pin_meta, meta_b) || !reserve_pinned(c, c->pin_x, xb) ||
+        !reserve_pinned(c, c->pin_y, ob) || (red && !reserve(c, c->red_out, ob)))
+        return 0;
+
+    uint8_t *hm = (uint8_t *)c->pin_meta.p;
+    ExpertDesc *hd = (ExpertDesc *)hm;
+    for (int i = 0; i < count; i++) {
+        hd[i].w[0] = gates[i]->w;
+        hd[i].w[1] = ups[i]->w;
+        hd[i].w[2] = downs[i]->w;
+        hd[i].sc[0] = gates[i]->sc;
+        hd[i].sc[1] = ups[i]->sc;
+        hd[i].sc[2] = downs[i]->sc;
+    }
+    int *hi = (int *)(hm + desc_b);
+    int *row_exp = hi, *mt_exp = row_exp + total, *mt_row0 = mt_exp + T, *mt_rend = mt_row0 + T;
+    int *counts = mt_rend + T;
+    int *rp = counts + 2, *ri = rp + (red ? s_n + 1 : 0);
+    float *rwv = (float *)(ri + (red ? total : 0));
+    for (int i = 0, r = 0, t = 0; i < count; i++) {
+        for (int q = 0; q < rows[i]; q++) row_exp[r + q] = i;
+        for (int q = 0; q < rows[i]; q += 32, t++) {
+            mt_exp[t] = i;
+            mt_row0[t] = r + q;
+            mt_rend[t] = r + rows[i];
+        }
+        r += rows[i];
+    }
+    counts[0] = total;
+    counts[1] = T;
+    if (red) {
+        std::memcpy(rp, red->row_ptr, (size_t)(s_n + 1) * 4);
+        std::memcpy(ri, red->row_idx, (size_t)total * 4);
+        std::memcpy(rwv, red->rw, (size_t)total * 4);
+    }
+    std::memcpy(c->pin_x.p, x, xb);
+
+    Prof prof(c);
+    prof.mark(-1);
+    uint8_t *dm = (uint8_t *)c->meta.p;
+    if (!hip_ok(hipMemcpyAsync(dm, hm, meta_b, hipMemcpyHostToDevice, c->stream), "expert group metadata"))
+        return 0;
+    // x ([total][D] f32) is staged in the y buffer, which has exactly that
+    // shape: the x quantisation reads it before the down projection writes y.
+    float *x_dev = (float *)c->y.p;
+    if (!hip_ok(hipMemcpyAsync(x_dev, c->pin_x.p, xb, hipMemcpyHostToDevice, c->stream), "expert group input upload"))
+        return 0;
+    int *di = (int *)(dm + desc_b);
+    RowPlan plan{};
+    plan.row_exp = di;
+    plan.row_act = di;   // unused: activation rows are the call's rows
+    plan.mt_exp = di + total;
+    plan.mt_row0 = di + total + T;
+    plan.mt_rend = di + total + 2 * T;
+    plan.counts = di + total + 3 * T;
+    run_experts(c, prof, (const ExpertDesc *)dm, plan, gg, gd, x_dev, total, true, total, T, ga, arm, s);
+    float *res = s.y;
+    if (red) {
+        const int *drp = plan.counts + 2, *dri = drp + s_n + 1;
+        const float *drw = (const float *)(dri + total);
+        prof.mark(COLI_HIP_K_COMBINE);
+        launch_combine((float *)c->red_out.p, s.y, drp, dri, drw, s_n, D, s.ys, c->stream);
+        res = (float *)c->red_out.p;
+    }
+    prof.mark(-1);
+    if (!hip_ok(hipGetLastError(), "expert group launch") ||
+        !hip_ok(hipMemcpyAsync(c->pin_y.p, res, ob, hipMemcpyDeviceToHost, c->stream), "expert group output download") ||
+        !hip_ok(hipStreamSynchronize(c->stream), "expert group synchronize"))
+        return 0;
+    prof.finish();
+    std::memcpy(red ? red->out : y, c->pin_y.p, ob);
+    note_group(count, total);
+    return 1;
+}
+
+}  // namespace
+
+// ============================================================================
+// C ABI
+// ============================================================================
+extern "C" {
+
+int coli_hip_init(const int *devices, int count) {
+    int available = 0;
+    if (!devices || count < 1 || count > COLI_HIP_MAX_DEVICES) return 0;
+    if (!hip_ok(hipGetDeviceCount(&available), "device discovery")) return 0;
+    for (int i = 0; i < g_nctx; i++) free_ctx(&g_ctx[i]);
+    g_nctx = 0;
+    g_cur_dev = -1;
+    for (int i = 0; i < count; i++) {
+        const int device = devices[i];
+        if (device < 0 || device >= available) {
+            std::fprintf(stderr, "[HIP] invalid device %d (available: 0..%d)\n", device, available - 1);
+            for (int j = 0; j < g_nctx; j++) free_ctx(&g_ctx[j]);
+            g_nctx = 0;
+            return 0;
+        }
+        if (find_ctx(device)) {
+            std::fprintf(stderr, "[HIP] duplicate device %d\n", device);
+            for (int j = 0; j < g_nctx; j++) free_ctx(&g_ctx[j]);
+            g_nctx = 0;
+            return 0;
+        }
+        Ctx *c = &g_ctx[g_nctx];
+        *c = Ctx{};
+        c->device = device;
+        if (!select_ctx(c)) return 0;
+        hipDeviceProp_t prop{};
+        if (!hip_ok(hipGetDeviceProperties(&prop, device), "device properties") ||
+            !hip_ok(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "stream creation")) {
+            for (int j = 0; j < g_nctx; j++) free_ctx(&g_ctx[j]);
+            g_nctx = 0;
+            return 0;
+        }
+        g_nctx++;
+        std::fprintf(stderr, "[HIP] device %d: %s (%s), %.1f GB HBM, %d CUs\n", device, prop.name, prop.gcnArchName,
+                     prop.totalGlobalMem / 1e9, prop.multiProcessorCount);
+    }
+    return 1;
+}
+
+void coli_hip_shutdown(void) {
+    for (int i = 0; i < g_nctx; i++) {
+        if (!select_ctx(&g_ctx[i])) continue;
+        free_ctx(&g_ctx[i]);
+    }
+    g_nctx = 0;
+    g_cur_dev = -1;
+}
+
+int coli_hip_device_count(void) { return g_nctx; }
+
+int coli_hip_probe_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n < 0) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return n;
+}
+
+int coli_hip_device_at(int index) { return index >= 0 && index < g_nctx ? g_ctx[index].device : -1; }
+
+int coli_hip_mem_info(int device, size_t *free_bytes, size_t *total_bytes) {
+    Ctx *c = find_ctx(device);
+    if (!free_bytes || !total_bytes || !select_ctx(c)) return 0;
+    return hip_ok(hipMemGetInfo(free_bytes, total_bytes), "memory info");
+}
+
+void coli_hip_stats(int device, size_t *tensor_count, size_t *tensor_bytes) {
+    size_t n = 0, b = 0;
+    for (int i = 0; i < g_nctx; i++)
+        if (device < 0 || g_ctx[i].device == device) {
+            n += g_ctx[i].tensor_count;
+            b += g_ctx[i].tensor_bytes;
+        }
+    if (tensor_count) *tensor_count = n;
+    if (tensor_bytes) *tensor_bytes = b;
+}
+
+void coli_hip_group_stats(uint64_t *calls, uint64_t *experts, uint64_t *rows, double *h2d_ms, double *kernel_ms,
+                          double *d2h_ms) {
+    std::lock_guard<std::mutex> lock(g_stats_mu);
+    if (calls) *calls = g_calls;
+    if (experts) *experts = g_experts;
+    if (rows) *rows = g_rows;
+    if (h2d_ms) *h2d_ms = g_h2d_ms;
+    if (kernel_ms) {
+        double k = 0;
+        for (int i = 0; i < COLI_HIP_K_COUNT; i++) k += g_k_ms[i];
+        *kernel_ms = k;
+    }
+    if (d2h_ms) *d2h_ms = g_d2h_ms;
+}
+
+int coli_hip_tensor_upload(ColiHipTensor **tensor, const void *weights, const float *scales, int fmt, int I, int O,
+                           int device) {
+    if (fmt != COLI_HIP_FMT_I8 && fmt != COLI_HIP_FMT_I4)
+        return fail("tensor_upload takes per-row formats 1 and 2; use tensor_upload_grouped");
+    return upload_impl(tensor, weights, scales, fmt, I, O, 0, device, false);
+}
+
+int coli_hip_tensor_upload_grouped(ColiHipTensor **tensor, const void *weights, const float *scales, int fmt, int I,
+                                   int O, int gs, int device) {
+    return upload_impl(tensor, weights, scales, fmt, I, O, gs, device, false);
+}
+
+int coli_hip_tensor_upload_dev(ColiHipTensor **tensor, const void *weights_dev, const float *scales_dev, int fmt,
+                               int I, int O, int gs, int device) {
+    return upload_impl(tensor, weights_dev, scales_dev, fmt, I, O, gs, device, true);
+}
+
+void coli_hip_tensor_free(ColiHipTensor *t) {
+    if (!t) return;
+    Ctx *c = find_ctx(t->device);
+    if (c) {
+        select_ctx(c);
+        c->tensor_count--;
+        c->tensor_bytes -= t->w_bytes + t->sc_bytes;
+    }
+    tensor_release(t);
+}
+
+size_t coli_hip_tensor_bytes(const ColiHipTensor *t) { return t ? t->w_bytes + t->sc_bytes : 0; }
+
+int coli_hip_tensor_device(const ColiHipTensor *t) { return t ? t->device : -1; }
+
+int coli_hip_tensor_update(ColiHipTensor *t, const void *weights, const float *scales) {
+    if (!t || !weights || !scales) return 0;
+    Ctx *c = find_ctx(t->device);
+    if (!select_ctx(c)) return 0;
+    return repack_from_host(c, t, weights, scales);
+}
+
+int coli_hip_expert_group(ColiHipTensor *const *gates, ColiHipTensor *const *ups, ColiHipTensor *const *downs,
+                          const int *rows, int count, float *y, const float *x) {
+    return expert_group_impl(gates, ups, downs, rows, count, y, x, nullptr, nullptr);
+}
+
+int coli_hip_expert_group_tiled(ColiHipTensor *const *gates, ColiHipTensor *const *ups,
+                                ColiHipTensor *const *downs, const int *rows, int count, float *y, const float *x,
+                                int tile_m, int tile_n, int tile_k, int *arm_out) {
+    (void)tile_m;
+    (void)tile_n;
+    (void)tile_k;
+    return expert_group_impl(gates, ups, downs, rows, count, y, x, nullptr, arm_out);
+}
+
+int coli_hip_expert_group_reduce(ColiHipTensor *const *gates, ColiHipTensor *const *ups,
+                                 ColiHipTensor *const *downs, const int *rows, int count, const int *row_ptr,
+                                 const int *row_idx, const float *rw, int s_n, float *out, const float *x) {
+    ReduceSpec red{row_ptr, row_idx, rw, s_n, out};
+    return expert_group_impl(gates, ups, downs, rows, count, nullptr, x, &red, nullptr);
+}
+
+int coli_hip_graph_begin(int device) {
+    Ctx *c = find_ctx(device);
+    if (!select_ctx(c)) return 0;
+    return hip_ok(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "graph begin capture");
+}
+
+int coli_hip_graph_end(int device, ColiHipGraph **out) {
+    Ctx *c = find_ctx(device);
+    if (!out || !select_ctx(c)) return 0;
+    hipGraph_t graph = nullptr;
+    if (!hip_ok(hipStreamEndCapture(c->stream, &graph), "graph end capture")) return 0;
+    hipGraphExec_t exec = nullptr;
+    if (!hip_ok(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "graph instantiate")) {
+        hipGraphDestroy(graph);
+        return 0;
+    }
+    ColiHipGraph *g = (ColiHipGraph *)std::calloc(1, sizeof(ColiHipGraph));
+    if (!g) {
+        hipGraphExecDestroy(exec);
+        hipGraphDestroy(graph);
+        return 0;
+    }
+    g->graph = graph;
+    g->exec = exec;
+    g->device = device;
+    *out = g;
+    return 1;
+}
+
+int coli_hip_graph_launch(ColiHipGraph *g) {
+    if (!g) return 0;
+    Ctx *c = find_ctx(g->device);
+    if (!select_ctx(c)) return 0;
+    if (!hip_ok(hipGraphLaunch(g->exec, c->stream), "graph launch")) return 0;
+    return hip_ok(hipStreamSynchronize(c->stream), "graph synchronize");
+}
+
+void coli_hip_graph_free(ColiHipGraph *g) {
+    if (!g) return;
+    if (g->exec) hipGraphExecDestroy(g->exec);
+    if (g->graph) hipGraphDestroy(g->graph);
+    std::free(g);
+}
+
+void coli_hip_graph_cache_stats(uint64_t *captures, uint64_t *replays, uint64_t *invalidations,
+                                uint64_t *uncacheable) {
+    std::lock_guard<std::mutex> lock(g_stats_mu);
+    if (captures) *captures = g_graph_captures;
+    if (replays) *replays = g_graph_replays;
+    if (invalidations) *invalidations = g_graph_invalidations;
+    if (uncacheable) *uncacheable = g_graph_uncacheable;
+}
+
+int coli_hip_pipe_sync(int device) {
+    Ctx *c = find_ctx(device);
+    if (!select_ctx(c)) return 0;
+    return hip_ok(hipStreamSynchronize(c->stream), "stream synchronize");
+}
+
+void *coli_hip_pipe_alloc(int device, size_t bytes) {
+    Ctx *c = find_ctx(device);
+    void *p = nullptr;
+    if (!select_ctx(c) || bytes == 0) return nullptr;
+    if (!hip_ok(hipMalloc(&p, bytes), "pipe allocation")) return nullptr;
+    return p;
+}
+
+void coli_hip_pipe_free(int device, void *p) {
+    Ctx *c = find_ctx(device);
+    if (!p || !select_ctx(c)) return;
+    hipStreamSynchronize(c->stream);
+    hipFree(p);
+}
+
+int coli_hip_pipe_upload(int device, void *dst, const void *src, size_t bytes) {
+    Ctx *c = find_ctx(device);
+    if (!dst || !src || !select_ctx(c)) return 0;
+    return hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream), "pipe upload") &&
+           hip_ok(hipStreamSynchronize(c->stream), "pipe upload sync");
+}
+
+int coli_hip_pipe_download(int device, const void *src, void *dst, size_t bytes) {
+    Ctx *c = find_ctx(device);
+    if (!dst || !src || !select_ctx(c)) return 0;
+    return hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream), "pipe download") &&
+           hip_ok(hipStreamSynchronize(c->stream), "pipe download sync");
+}
+
+int coli_hip_event_record(int device, int slot) {
+    Ctx *c = find_ctx(device);
+    if (slot < 0 || slot >= 16 || !select_ctx(c)) return 0;
+    if (!c->user_ev[slot] && !hip_ok(hipEventCreate(&c->user_ev[slot]), "event create")) return 0;
+    return hip_ok(hipEventRecord(c->user_ev[slot], c->stream), "event record");
+}
+
+float coli_hip_event_elapsed(int device, int a, int b) {
+    Ctx *c = find_ctx(device);
+    if (a < 0 || a >= 16 || b < 0 || b >= 16 || !select_ctx(c) || !c->user_ev[a] || !c->user_ev[b]) return -1.0f;
+    if (!hip_ok(hipEventSynchronize(c->user_ev[b]), "event sync")) return -1.0f;
+    float ms = -1.0f;
+    if (!hip_ok(hipEventElapsedTime(&ms, c->user_ev[a], c->user_ev[b]), "event elapsed")) return -1.0f;
+    return ms;
+}
+
+int coli_hip_synth_fill(int device, void *dst, size_t n, int kind, float a, float b, uint64_t seed) {
+    Ctx *c = find_ctx(device);
+    if (!dst || kind < 0 || kind > 2 || !select_ctx(c)) return 0;
+    launch_synth_fill(dst, n, kind, a, b, seed, c->stream);
+    return hip_ok(hipGetLastError(), "synthetic fill");
+}
+
+int coli_hip_set_act_group(int ga) {
+    if (ga != 0 && ga != 32) return fail("act group must be 0 (per row) or 32");
+    g_act_group = ga;
+    return 1;
+}
+
+int coli_hip_get_act_group(void) { return act_group(); }
+
+int coli_hip_set_arm(int arm) {
+    if (arm != -1 && arm != COLI_HIP_ARM_GEMV && arm != COLI_HIP_ARM_MFMA) return fail("unknown arm");
+    g_arm = arm;
+    return 1;
+}
+
+int coli_hip_set_profile(int on) {
+    g_profile = on ? 1 : 0;
+    return 1;
+}
+
+void coli_hip_kernel_stats(int which, uint64_t *launches, double *total_ms) {
+    std::lock_guard<std::mutex> lock(g_stats_mu);
+    const bool ok = which >= 0 && which < COLI_HIP_K_COUNT;
+    if (launches) *launches = ok ? g_k_launches[which] : 0;
+    if (total_ms) *total_ms = ok ? g_k_ms[which] : 0.0;
+}
+
+void coli_hip_reset_stats(void) {
+    std::lock_guard<std::mutex> lock(g_stats_mu);
+    g_calls = g_experts = g_rows = 0;
+    g_h2d_ms = g_kernel_ms = g_d2h_ms = 0;
+    for (int i = 0; i < COLI_HIP_K_COUNT; i++) {
+        g_k_launches[i] = 0;
+        g_k_ms[i] = 0;
+    }
+}
+
+int coli_hip_set_debug_dots(int32_t *gateup_dev, int32_t *down_dev) {
+    g_dbg_gu = gateup_dev;
+    g_dbg_dn = down_dev;
+    return 1;
+}
+
+int coli_hip_expert_set_create(ColiHipExpertSet **set, ColiHipTensor *const *gates, ColiHipTensor *const *ups,
+                               ColiHipTensor *const *downs, int count) {
+    if (!set) return 0;
+    int device = -1;
+    MatGeom gg{}, gd{};
+    if (!check_group(gates, ups, downs, count, &device, &gg, &gd)) return 0;
+    Ctx *c = find_ctx(device);
+    if (!select_ctx(c)) return 0;
+    std::vector<ExpertDesc> hd((size_t)count);
+    for (int i = 0; i < count; i++) {
+        hd[i].w[0] = gates[i]->w;
+        hd[i].w[1] = ups[i]->w;
+        hd[i].w[2] = downs[i]->w;
+        hd[i].sc[0] = gates[i]->sc;
+        hd[i].sc[1] = ups[i]->sc;
+        hd[i].sc[2] = downs[i]->sc;
+    }
+    ColiHipExpertSet *s = (ColiHipExpertSet *)std::calloc(1, sizeof(ColiHipExpertSet));
+    if (!s) return 0;
+    s->device = device;
+    s->count = count;
+    s->gg = gg;
+    s->gd = gd;
+    if (!hip_ok(hipMalloc(&s->desc_dev, sizeof(ExpertDesc) * count), "expert set allocation") ||
+        !hip_ok(hipMemcpy(s->desc_dev, hd.data(), sizeof(ExpertDesc) * count, hipMemcpyHostToDevice),
+                "expert set upload")) {
+        if (s->desc_dev) hipFree(s->desc_dev);
+        std::free(s);
+        return 0;
+    }
+    *set = s;
+    return 1;
+}
+
+void coli_hip_expert_set_free(ColiHipExpertSet *s) {
+    if (!s) return;
+    Ctx *c = find_ctx(s->device);
+    if (c) select_ctx(c);
+    if (s->desc_dev) hipFree(s->desc_dev);
+    std::free(s);
+}
+
+int coli_hip_route_softmax_topk_dev(int device, const float *logits_dev, int S, int E, int k, int *ids_dev,
+                                    float *w_dev) {
+    Ctx *c = find_ctx(device);
+    if (!logits_dev || !ids_dev || !w_dev || S < 1 || E < 1 || k < 1 || k > 16 || k > E || !select_ctx(c)) return 0;
+    launch_route_softmax(logits_dev, S, E, k, ids_dev, w_dev, c->stream);
+    return hip_ok(hipGetLastError(), "router launch");
+}
+
+int coli_hip_moe_forward_dev(const ColiHipExpertSet *set, const float *x_dev, int S, const int *ids_dev,
+                             const float *w_dev, int k, float *out_dev, int ga, int arm) {
+    if (!set || !x_dev || !ids_dev || !w_dev || !out_dev || S < 1 || k < 1) return 0;
+    if (k > 16) return fail("moe_forward: k > 16 is not supported");
+    if (set->count > 1024) return fail("moe_forward: more than 1024 experts");
+    if (ga != 0 && ga != 32) return fail("moe_forward: act group must be 0 or 32");
+    Ctx *c = find_ctx(set->device);
+    if (!select_ctx(c)) return 0;
+    const int E = set->count, R = S * k;
+    const int tmax = (R + 31) / 32 + std::min(E, R);
+    if (arm < 0) arm = forced_arm();
+    if (arm < 0) arm = S == 1 ? COLI_HIP_ARM_GEMV : COLI_HIP_ARM_MFMA;
+
+    // table layout in one buffer
+    const size_t n_int = 4 + (size_t)E + (E + 1) + 3 * (size_t)R + (size_t)(S + 1) + R + 3 * (size_t)tmax;
+    const size_t tbl_b = n_int * 4 + (size_t)R * 4;
+    Scratch s{};
+    if (!reserve_rows(c, set->gg, set->gd, S, R, ga, &s) || !reserve(c, c->tbl, tbl_b)) return 0;
+    int *p = (int *)c->tbl.p;
+    TableOut t{};
+    t.hdr = p;
+    p += 4;
+    t.uexp = p;
+    p += E;
+    t.off = p;
+    p += E + 1;
+    t.row_tok = p;
+    p += R;
+    t.row_kk = p;
+    p += R;
+    t.row_exp = p;
+    p += R;
+    t.tok_ptr = p;
+    p += S + 1;
+    t.tok_rows = p;
+    p += R;
+    t.mt_exp = p;
+    p += tmax;
+    t.mt_row0 = p;
+    p += tmax;
+    t.mt_rend = p;
+    p += tmax;
+    t.rw_row = (float *)p;
+    c->tbl_view = t;
+    c->tbl_E = E;
+    c->tbl_R = R;
+
+    Prof prof(c);
+    prof.mark(COLI_HIP_K_TABLE);
+    launch_build_table(ids_dev, w_dev, S, k, E, t, tmax, c->stream);
+    RowPlan plan{};
+    plan.row_exp = t.row_exp;
+    plan.row_act = t.row_tok;
+    plan.mt_exp = t.mt_exp;
+    plan.mt_row0 = t.mt_row0;
+    plan.mt_rend = t.mt_rend;
+    plan.counts = t.hdr;
+    run_experts(c, prof, set->desc_dev, plan, set->gg, set->gd, x_dev, S, false, R, tmax, ga, arm, s);
+    prof.mark(COLI_HIP_K_COMBINE);
+    launch_combine_padded(out_dev, s.y, t.tok_rows, t.rw_row, S, k, set->gd.O, s.ys, c->stream);
+    prof.mark(-1);
+    if (!hip_ok(hipGetLastError(), "moe forward launch")) return 0;
+    prof.finish();
+    note_group(E, R);
+    return 1;
+}
+
+void *coli_hip_stream(int device) {
+    Ctx *c = find_ctx(device);
+    return c ? (void *)c->stream : nullptr;
+}
+
+int coli_hip_last_table(int device, int *hdr, int *uexp, int *off, int *row_tok, int *tok_rows, int e_cap,
+                        int r_cap) {
+    Ctx *c = find_ctx(device);
+    if (!select_ctx(c) || !c->tbl_view.hdr) return 0;
+    const TableOut &t = c->tbl_view;
+    if (!hip_ok(hipStreamSynchronize(c->stream), "table sync")) return 0;
+    const int E = std::min(c->tbl_E, e_cap), R = std::min(c->tbl_R, r_cap);
+    int ok = 1;
+    if (hdr) ok &= hip_ok(hipMemcpy(hdr, t.hdr, 16, hipMemcpyDeviceToHost), "table copy");
+    if (uexp) ok &= hip_ok(hipMemcpy(uexp, t.uexp, (size_t)E * 4, hipMemcpyDeviceToHost), "table copy");
+    if (off) ok &= hip_ok(hipMemcpy(off, t.off, (size_t)(E + 1) * 4, hipMemcpyDeviceToHost), "table copy");
+    if (row_tok) ok &= hip_ok(hipMemcpy(row_tok, t.row_tok, (size_t)R * 4, hipMemcpyDeviceToHost), "table copy");
+    if (tok_rows) ok &= hip_ok(hipMemcpy(tok_rows, t.tok_rows, (size_t)R * 4, hipMemcpyDeviceToHost), "table copy");
+    return ok;
+}
+
+}  // extern "C"

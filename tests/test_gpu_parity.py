@@ -1,0 +1,344 @@
+"""GPU parity: the HIP lane through its C ABI against the CPU oracle.
+
+Bars: per-block int32 dots bit-exact; fp32 outputs
+within 1e-5 of the oracle, max-abs normalised. The kernels evaluate every f32
+epilogue in the oracle's order, so most cases are asserted bit-identical.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from peregrine_amd import qt, synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def nerr(got, ref):
+    ref = np.asarray(ref, np.float64)
+    den = max(np.max(np.abs(ref)), 1e-30)
+    return float(np.max(np.abs(np.asarray(got, np.float64) - ref)) / den)
+
+
+@pytest.fixture(scope="module")
+def hip():
+    from peregrine_amd import hip as h
+    assert h.probe_device_count() >= 1
+    assert h.init([0]) == 1
+    yield h
+    h.set_arm(-1)
+    h.set_act_group(0)
+    h.set_debug_dots(0, 0)
+
+
+def _experts(rng, n, D, I, fmt, gs, orc, hip):
+    gpu, ora = [], []
+    for _ in range(n):
+        trip = synth.make_expert(rng, D, I, fmt, gs)
+        gpu.append(hip.GpuExpert.upload_grouped(0, trip[0][:2], trip[1][:2], trip[2][:2], D, I, fmt, gs))
+        shp = ((I, D), (I, D), (D, I))
+        ora.append(tuple(orc.Tensor(t[0], t[1], fmt, i, o, gs) for t, (o, i) in zip(trip, shp)))
+    return gpu, ora
+
+
+def test_probe_init_meminfo(hip):
+    assert hip.device_count() == 1
+    free, total = hip.mem_info(0)
+    assert total > 100e9 and 0 < free <= total
+
+
+FORMATS = [(qt.FMT_I4G, 32), (qt.FMT_I4G, 128), (qt.FMT_I4, 0), (qt.FMT_I8G, 32), (qt.FMT_I8, 0)]
+
+
+@pytest.mark.parametrize("fmt,gs", FORMATS)
+@pytest.mark.parametrize("ga", [0, 32])
+@pytest.mark.parametrize("arm", [2, 0])
+def test_expert_group_matches_oracle(hip, orc, fmt, gs, ga, arm):
+    say("expert_group", fmt, gs, ga, arm)
+    rng = np.random.default_rng(100 + fmt * 7 + gs + ga + arm)
+    D, I = 320, 192   # not multiples of the 64-row tile: exercises padding
+    gpu, ora = _experts(rng, 3, D, I, fmt, gs or 32, orc, hip)
+    rows = [1, 3, 34]
+    x = rng.standard_normal((sum(rows), D)).astype(np.float32)
+    hip.set_act_group(ga)
+    hip.set_arm(arm)
+    y, used = hip.expert_group_tiled(gpu, rows, x, D)
+    assert used.value == arm
+    r0 = 0
+    for e, n in enumerate(rows):
+        ref = orc.expert_swiglu(x[r0:r0 + n], *ora[e], ga)
+        assert nerr(y[r0:r0 + n], ref) <= TOL, (e, nerr(y[r0:r0 + n], ref))
+        assert np.array_equal(y[r0:r0 + n], ref), f"expert {e}: not bit-identical"
+        r0 += n
+
+
+@pytest.mark.parametrize("arm", [2, 0])
+@pytest.mark.parametrize("fmt", [qt.FMT_I4G, qt.FMT_I8G])
+def test_block_dots_bit_exact(hip, orc, arm, fmt):
+    say("block dots", arm, fmt)
+    rng = np.random.default_rng(7 + arm + fmt)
+    D, I = 256, 128
+    gpu, ora = _experts(rng, 2, D, I, fmt, 32, orc, hip)
+    rows = [2, 3]
+    R = sum(rows)
+    x = rng.standard_normal((R, D)).astype(np.float32)
+    nbd, nbi = D // 32, I // 32
+    dgu = hip.DeviceBuffer(R * 2 * I * nbd * 4)
+    ddn = hip.DeviceBuffer(R * D * nbi * 4)
+    hip.set_act_group(32)
+    hip.set_arm(arm)
+    hip.set_debug_dots(dgu.ptr, ddn.ptr)
+    try:
+        hip.expert_group(gpu, rows, x, D)
+    finally:
+        hip.set_debug_dots(0, 0)
+    gu = dgu.download(np.int32, (R, 2, I, nbd))
+    dn = ddn.download(np.int32, (R, D, nbi))
+    r0 = 0
+    for e, n in enumerate(rows):
+        xq, sx = orc.quant_rows(x[r0:r0 + n], 32)
+        assert np.array_equal(gu[r0:r0 + n, 0], orc.block_dots(xq, ora[e][0]))
+        assert np.array_equal(gu[r0:r0 + n, 1], orc.block_dots(xq, ora[e][1]))
+        _, h = orc.expert_swiglu(x[r0:r0 + n], *ora[e], 32, want_h=True)
+        hq, _ = orc.quant_rows(h, 32)
+        assert np.array_equal(dn[r0:r0 + n], orc.block_dots(hq, ora[e][2]))
+        r0 += n
+
+
+@pytest.mark.parametrize("ga", [0, 32])
+def test_expert_group_reduce(hip, orc, ga):
+    say("expert_group_reduce", ga)
+    rng = np.random.default_rng(21 + ga)
+    D, I = 256, 128
+    gpu, ora = _experts(rng, 3, D, I, qt.FMT_I4G, 32, orc, hip)
+    rows = [2, 1, 3]
+    x = rng.standard_normal((6, D)).astype(np.float32)
+    dst = [0, 1, 0, 1, 0, 1]
+    rw = rng.uniform(0.1, 1.0, 6).astype(np.float32)
+    lay = hip.ReduceLayout.build(dst, 2)
+    assert list(lay.row_ptr) == [0, 3, 6]
+    hip.set_act_group(ga)
+    hip.set_arm(-1)
+    out = hip.expert_group_reduce(gpu, rows, x, D, lay, rw, 2)
+    y = hip.expert_group(gpu, rows, x, D)
+    ref = orc.grouped_reduce(y, lay.row_ptr, lay.row_idx, rw, 2)
+    assert np.array_equal(out, ref)
+    # repeat: no atomics, so the result is bit-stable
+    assert np.array_equal(out, hip.expert_group_reduce(gpu, rows, x, D, lay, rw, 2))
+
+
+def test_expert_group_error_paths(hip, orc):
+    say("error paths")
+    rng = np.random.default_rng(3)
+    gpu, _ = _experts(rng, 2, 64, 64, qt.FMT_I4G, 32, orc, hip)
+    x = np.zeros((2, 64), np.float32)
+    with pytest.raises(hip.HipError):
+        hip.expert_group(gpu, [1, 0], x[:1], 64)
+    with pytest.raises(hip.HipError):
+        hip.expert_group(gpu, [1], x, 64)
+    with pytest.raises(hip.HipError):
+        hip.expert_group(gpu, [1, 1], x[:1], 64)
+    with pytest.raises(hip.HipError):
+        hip.expert_group([gpu[0]] * 257, [1] * 257, np.zeros((257, 64), np.float32), 64)
+    q, sc, _ = synth.make_tensor(rng, 64, 64, qt.FMT_I4G, 32)
+    with pytest.raises(hip.HipError):
+        hip._upload(0, q, sc, qt.FMT_I4G, 64, 64, 48)     # unsupported group size
+    with pytest.raises(hip.HipError):
+        hip._upload(0, q, sc, 3, 64, 64, 0)                # int2 not resident here
+    with pytest.raises(hip.HipError):
+        hip.GpuExpert.upload(0, None, None, None, 64, 64)
+    assert hip.ReduceLayout.build([0, 2], 2) is None
+    # an expert whose down shape disagrees is rejected before any launch
+    other, _ = _experts(rng, 1, 64, 32, qt.FMT_I4G, 32, orc, hip)
+    mixed = hip.GpuExpert(gpu[0].gate, gpu[0].up, other[0].down, 64, 64)
+    try:
+        with pytest.raises(hip.HipError):
+            hip.expert_group([mixed], [1], x[:1], 64)
+    finally:
+        mixed.gate = mixed.up = mixed.down = None
+
+
+def test_tensor_update_changes_results(hip, orc):
+    say("tensor_update")
+    rng = np.random.default_rng(5)
+    D, I = 128, 64
+    gpu, ora = _experts(rng, 1, D, I, qt.FMT_I4, 0, orc, hip)
+    x = rng.standard_normal((1, D)).astype(np.float32)
+    hip.set_act_group(0)
+    y0 = hip.expert_group(gpu, [1], x, D)
+    q, sc, _ = synth.make_tensor(rng, I, D, qt.FMT_I4, 0)
+    from peregrine_amd._lib import lib
+    import ctypes as C
+    assert lib.coli_hip_tensor_update(gpu[0].gate, C.c_void_p(q.ctypes.data), C.c_void_p(sc.ctypes.data)) == 1
+    y1 = hip.expert_group(gpu, [1], x, D)
+    ref = orc.expert_swiglu(x, orc.Tensor(q, sc, qt.FMT_I4, D, I), ora[0][1], ora[0][2], 0)
+    assert not np.array_equal(y0, y1) and np.array_equal(y1, ref)
+
+
+# ------------------------------------------------------------ device-resident MoE layer
+
+def _layer_case(hip, orc, rng, E, D, I, S, k, fmt=qt.FMT_I4G, gs=32, zipf=False):
+    gpu, ora = _experts(rng, E, D, I, fmt, gs, orc, hip)
+    eset = hip.ExpertSet(gpu)
+    x = rng.standard_normal((S, D)).astype(np.float32)
+    logits = synth.zipf_logits(rng, S, E) if zipf else synth.normal_logits(rng, S, E)
+    return gpu, ora, eset, x, logits
+
+
+def _run_layer(hip, eset, x, logits, k, ga, arm):
+    S, D = x.shape
+    E = logits.shape[1]
+    bx = hip.DeviceBuffer.from_array(x)
+    bl = hip.DeviceBuffer.from_array(logits)
+    bids = hip.DeviceBuffer(S * k * 4)
+    bw = hip.DeviceBuffer(S * k * 4)
+    bout = hip.DeviceBuffer(S * D * 4)
+    hip.route_softmax_topk_dev(0, bl.ptr, S, E, k, bids.ptr, bw.ptr)
+    hip.moe_forward_dev(eset, bx.ptr, S, bids.ptr, bw.ptr, k, bout.ptr, ga, arm)
+    hip.pipe_sync(0)
+    return (bout.download(np.float32, (S, D)), bids.download(np.int32, (S, k)), bw.download(np.float32, (S, k)))
+
+
+def test_router_matches_oracle(hip, orc):
+    say("router")
+    rng = np.random.default_rng(8)
+    for S, E, k in ((1, 160, 8), (37, 256, 8), (5, 7, 3)):
+        logits = synth.normal_logits(rng, S, E)
+        logits[0, 3] = logits[0, 5] = np.max(logits[0]) + 1.0   # a tie: lower index first
+        bl = hip.DeviceBuffer.from_array(logits)
+        bids, bw = hip.DeviceBuffer(S * k * 4), hip.DeviceBuffer(S * k * 4)
+        hip.route_softmax_topk_dev(0, bl.ptr, S, E, k, bids.ptr, bw.ptr)
+        hip.pipe_sync(0)
+        idx, w = orc.route_softmax_topk(logits, k)
+        assert np.array_equal(bids.download(np.int32, (S, k)), idx)
+        assert np.array_equal(bw.download(np.float32, (S, k)), w)
+        assert list(idx[0][:2]) == [3, 5]
+
+
+@pytest.mark.parametrize("ga", [0, 32])
+@pytest.mark.parametrize("arm", [2, 0])
+def test_moe_layer_matches_oracle(hip, orc, ga, arm):
+    say("moe layer", ga, arm)
+    rng = np.random.default_rng(40 + ga + arm)
+    E, D, I, S, k = 12, 256, 192, 19, 4
+    gpu, ora, eset, x, logits = _layer_case(hip, orc, rng, E, D, I, S, k, zipf=True)
+    out, ids, w = _run_layer(hip, eset, x, logits, k, ga, arm)
+    ref = orc.moe_forward(x, ids, w, ora, ga)
+    assert nerr(out, ref) <= TOL
+    assert np.array_equal(out, ref)
+    # the device-built expert-offset table equals the oracle's
+    t = hip.last_table(0, E, S * k)
+    o = orc.expert_table(ids, E)
+    assert t["n_u"] == o["n_u"] and np.array_equal(t["uexp"], o["uexp"]) and np.array_equal(t["off"], o["off"])
+    assert np.array_equal(t["row_tok"], o["row_tok"])
+    assert np.array_equal(t["tok_rows"].reshape(S, k), o["tok_rows"])
+
+
+def test_moe_layer_arms_agree_and_repeat(hip, orc):
+    say("arms agree")
+    rng = np.random.default_rng(77)
+    E, D, I, S, k = 10, 192, 128, 6, 3
+    gpu, ora, eset, x, logits = _layer_case(hip, orc, rng, E, D, I, S, k)
+    a, _, _ = _run_layer(hip, eset, x, logits, k, 32, 2)
+    b, _, _ = _run_layer(hip, eset, x, logits, k, 32, 0)
+    c, _, _ = _run_layer(hip, eset, x, logits, k, 32, 0)
+    assert np.array_equal(a, b) and np.array_equal(b, c)
+
+
+@pytest.mark.parametrize("ga", [32, 0])
+def test_decode_layer_full_shape(hip, orc, ga):
+    """BASELINE config 2 shape (D=5120, I=1536, top-8) with 16 resident experts."""
+    say("decode full shape", ga)
+    rng = np.random.default_rng(2024 + ga)
+    E, D, I, S, k = 16, 5120, 1536, 1, 8
+    gpu, ora, eset, x, logits = _layer_case(hip, orc, rng, E, D, I, S, k)
+    out, ids, w = _run_layer(hip, eset, x, logits, k, ga, -1)
+    ref = orc.moe_forward(x, ids, w, ora, ga)
+    assert nerr(out, ref) <= TOL, nerr(out, ref)
+
+
+def test_batched_layer_full_width_sampled(hip, orc):
+    """BASELINE config 3 widths (64 tokens, Zipf top-8), checked on 6 sampled tokens."""
+    say("batched 64 tokens")
+    rng = np.random.default_rng(64)
+    E, D, I, S, k = 24, 5120, 1536, 64, 8
+    gpu, ora, eset, x, logits = _layer_case(hip, orc, rng, E, D, I, S, k, zipf=True)
+    out, ids, w = _run_layer(hip, eset, x, logits, k, 32, -1)
+    sub = np.array([0, 5, 17, 33, 48, 63])
+    ref = orc.moe_forward(x, ids, w, ora, 32, subset=sub, nthreads=8)
+    assert nerr(out[sub], ref[sub]) <= TOL
+
+
+def test_graph_replay_matches_eager(hip, orc):
+    say("graph replay")
+    rng = np.random.default_rng(91)
+    E, D, I, S, k = 8, 256, 128, 3, 2
+    gpu, ora, eset, x, logits = _layer_case(hip, orc, rng, E, D, I, S, k)
+    bx = hip.DeviceBuffer.from_array(x)
+    bl = hip.DeviceBuffer.from_array(logits)
+    bids, bw, bout = hip.DeviceBuffer(S * k * 4), hip.DeviceBuffer(S * k * 4), hip.DeviceBuffer(S * D * 4)
+
+    def body():
+        hip.route_softmax_topk_dev(0, bl.ptr, S, E, k, bids.ptr, bw.ptr)
+        hip.moe_forward_dev(eset, bx.ptr, S, bids.ptr, bw.ptr, k, bout.ptr, 32, -1)
+
+    body()   # eager first: reserves every scratch buffer the capture will bake in
+    hip.pipe_sync(0)
+    eager = bout.download(np.float32, (S, D))
+    g = hip.capture(0, body)
+    for rep in range(4):
+        x2 = rng.standard_normal((S, D)).astype(np.float32)
+        bx.upload(x2)
+        g.launch()
+        got = bout.download(np.float32, (S, D))
+        body()
+        hip.pipe_sync(0)
+        assert np.array_equal(got, bout.download(np.float32, (S, D))), rep
+    bx.upload(x)
+    g.launch()
+    assert np.array_equal(bout.download(np.float32, (S, D)), eager)
+
+
+def test_greedy_argmax_token_identical(hip, orc):
+    """Random-init MoE-only stack (embedding -> 3 MoE layers with residual ->
+    lm_head argmax); the GPU and the oracle generate the same tokens."""
+    say("greedy argmax")
+    rng = np.random.default_rng(0xC0FFEE)
+    V, D, I, E, k, L, B, steps = 64, 128, 64, 8, 2, 3, 4, 12
+    emb = rng.standard_normal((V, D)).astype(np.float32)
+    head = rng.standard_normal((V, D)).astype(np.float32)
+    layers = []
+    for _ in range(L):
+        gpu, ora = _experts(rng, E, D, I, qt.FMT_I4G, 32, orc, hip)
+        router = (rng.standard_normal((E, D)) * 0.1).astype(np.float32)
+        layers.append((hip.ExpertSet(gpu), gpu, ora, router))
+    tok_g = rng.integers(0, V, B)
+    tok_o = tok_g.copy()
+    seq_g, seq_o = [], []
+    for _ in range(steps):
+        for side in ("gpu", "ora"):
+            tok = tok_g if side == "gpu" else tok_o
+            x = emb[tok].copy()
+            for eset, gpu, ora, router in layers:
+                logits = orc.matmul_f32(x, router, D, E)
+                if side == "gpu":
+                    out, _, _ = _run_layer(hip, eset, x, logits, k, 0, -1)
+                else:
+                    ids, w = orc.route_softmax_topk(logits, k)
+                    out = orc.moe_forward(x, ids, w, ora, 0)
+                x = (x + out).astype(np.float32)
+            nxt = np.argmax(orc.matmul_f32(x, head, D, V), axis=1)
+            if side == "gpu":
+                tok_g = nxt
+                seq_g.append(nxt)
+            else:
+                tok_o = nxt
+                seq_o.append(nxt)
+    assert np.array_equal(np.array(seq_g), np.array(seq_o))
