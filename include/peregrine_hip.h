@@ -137,6 +137,11 @@ int coli_hip_route_softmax_topk_dev(int device, const float *logits_dev, int S, 
  * Async on the device stream (coli_hip_pipe_sync waits). */
 int coli_hip_moe_forward_dev(const ColiHipExpertSet *set, const float *x_dev, int S, const int *ids_dev,
                              const float *w_dev, int k, float *out_dev, int act_group, int arm);
+/* Same layer with the router fused in: logits[S][E] (device) are routed
+ * (as coli_hip_route_softmax_topk_dev) into ids_dev/w_dev [S][k], then the
+ * layer runs. One token (S = 1) on the GEMV arm needs no expert table. */
+int coli_hip_moe_forward_logits_dev(const ColiHipExpertSet *set, const float *x_dev, int S, const float *logits_dev,
+                                    int k, int *ids_dev, float *w_dev, float *out_dev, int act_group, int arm);
 /* The device stream (hipStream_t) of an initialised device, for interop. */
 void *coli_hip_stream(int device);
 
@@ -157,6 +162,11 @@ void coli_hip_reset_stats(void);
  * also write every per-32-block int32 dot they compute: gate/up as
  * [R][2][I][ceil(D/32)], down as [R][D][ceil(I/32)]. */
 int coli_hip_set_debug_dots(int32_t *gateup_dev, int32_t *down_dev);
+/* Tuning hook: when set (device pointers, may be NULL), GEMV-arm workgroups
+ * write 8 int64 per workgroup (index y*grid_x + x): phase timestamps of the
+ * 100 MHz constant clock (entry, first weights in, blocks done, barrier,
+ * chain done, exit) and the hardware CU id. */
+int coli_hip_set_debug_trace(long long *gateup_dev, long long *down_dev);
 /* Last row plan of the device-resident path, copied to host (for tests):
  * hdr[4] = {rows, tiles, distinct experts, 0}. */
 int coli_hip_last_table(int device, int *hdr, int *uexp, int *off, int *row_tok, int *tok_rows, int e_cap,

@@ -66,11 +66,13 @@ SIGNATURES = {
     "coli_hip_expert_set_free": (None, [_p]),
     "coli_hip_route_softmax_topk_dev": (_i, [_i, _p, _i, _i, _i, _p, _p]),
     "coli_hip_moe_forward_dev": (_i, [_p, _p, _i, _p, _p, _i, _p, _i, _i]),
+    "coli_hip_moe_forward_logits_dev": (_i, [_p, _p, _i, _p, _i, _p, _p, _p, _i, _i]),
     "coli_hip_stream": (_p, [_i]),
     "coli_hip_set_profile": (_i, [_i]),
     "coli_hip_kernel_stats": (None, [_i, _u64p, _dp]),
     "coli_hip_reset_stats": (None, []),
     "coli_hip_set_debug_dots": (_i, [_p, _p]),
+    "coli_hip_set_debug_trace": (_i, [_p, _p]),
     "coli_hip_last_table": (_i, [_i, _ip, _ip, _ip, _ip, _ip, _i, _i]),
 }
 

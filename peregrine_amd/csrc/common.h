@@ -54,6 +54,7 @@ struct MatGeom {
     int K, Kp, nb;         // inputs, inputs padded to 32, blocks
     int O, Op;             // outputs, outputs padded to 64
     int gpb, ng;           // blocks per weight group, groups (per-row: gpb = nb, ng = 1)
+    int gshift;            // log2(gpb) for grouped weights; 30 for per-row (every block maps to group 0)
     int w4;                // 1: int4 weights, 0: int8
     int per_row;           // weight scale per row
 };
@@ -66,9 +67,51 @@ struct RowPlan {
     const int *mt_row0;    // [T] first row of the tile
     const int *mt_rend;    // [T] one past the last row of that expert
     const int *counts;     // [2] {R, T} as built on the device (or host)
+    const ExpertDesc *row_desc;  // optional [R]: row r's descriptor, written by the router
 };
 
 // ---- device helpers ----
+
+// Address-space hints: pointers read from descriptor tables are generic; cast
+// them so loads are emitted as global (not flat) memory operations.
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T *gptr(const T *p) {
+    return (const __attribute__((address_space(1))) T *)p;
+}
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T *gptr_w(T *p) {
+    return (__attribute__((address_space(1))) T *)p;
+}
+
+// Phase timestamp for the optional kernel trace (100 MHz constant clock),
+// taken after every outstanding memory operation of the wave has completed.
+__device__ __forceinline__ long long trace_stamp() {
+    __builtin_amdgcn_s_waitcnt(0);
+    return (long long)__builtin_amdgcn_s_memrealtime();
+}
+
+// Buffer-resource loads: a uniform descriptor (base, byte range) in SGPRs, a
+// 32-bit per-lane offset and a uniform 32-bit offset. No 64-bit address math
+// per load, and reads past the range return zero instead of faulting.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ float bloadf(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+
+// Index of the wavefront in its workgroup, known to the compiler as uniform.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// Weight group of block b and whether b closes its group.
+__device__ __forceinline__ int grp_of(int b, int gshift) { return gshift >= 30 ? 0 : b >> gshift; }
+__device__ __forceinline__ bool grp_end(int b, int gshift, int nb) {
+    return b + 1 == nb || (gshift < 30 && ((b + 1) & ((1 << gshift) - 1)) == 0);
+}
 
 // exp rounded once to f32 from a double-precision exp; equal to the correctly
 // rounded expf except within ~2^-28 of a midpoint. The oracle does the same.
@@ -148,6 +191,10 @@ struct DotArgs {   // shared by the GEMV and MFMA arms
     int8_t *hq; int hq_stride; float *sh; int sh_stride;                // fused h quant (ACT_B32)
     int32_t *dots;                                                      // optional per-block dot dump
     int act_identity;                                                   // activation row = r (down proj)
+    int act_zero;                                                       // activation row = 0 (one token)
+    int n_rows_fixed;                                                   // >= 0: row count known on the host
+    long long *trace;                                                   // optional phase timestamps (tests/tuning)
+    int buf_ok;   // every expert's gate/up tiles lie within one 4 GB buffer window
 };
 // grid_rows / grid_tiles: host-side upper bounds; the kernels read the true
 // counts from plan.counts and idle the excess workgroups.
@@ -158,19 +205,21 @@ void launch_mfma_down(const DotArgs &a, const MatGeom &g, int act, int grid_tile
 
 void launch_combine(float *out, const float *y, const int *row_ptr, const int *row_idx, const float *rw,
                     int s_n, int D, int y_stride, hipStream_t st);
-void launch_combine_padded(float *out, const float *y, const int *tok_rows, const float *rw, int s_n, int k, int D,
-                           int y_stride, hipStream_t st);
+void launch_combine_tok(float *out, const float *y, const int *tok_rows, const int *tok_kk, const float *w, int s_n,
+                        int k, int D, int y_stride, hipStream_t st);
 void launch_route_softmax(const float *logits, int S, int E, int k, int *ids, float *w, hipStream_t st);
+void launch_route_quant(const float *logits, int S, int E, int k, int *ids, float *w, const QuantArgs &a,
+                        const ExpertDesc *desc, ExpertDesc *row_desc, hipStream_t st);
+// LDS bytes one workgroup may use (device attribute), set at init.
+void set_lds_limit(int bytes);
 
 struct TableOut {
     int *hdr;          // [4]: R, T, n_u, flags
     int *uexp, *off;   // [E], [E+1]
     int *row_tok, *row_kk, *row_exp;  // [R]
-    int *tok_ptr, *tok_rows;          // [S+1], [S*k] (CSR of each token's rows, union order)
-    float *rw_row;     // [R]
+    int *tok_rows, *tok_kk;           // [S*k]: each token's rows in union order (-1 pads), their top-k slot
     int *mt_exp, *mt_row0, *mt_rend;  // [Tmax]
 };
 void launch_synth_fill(void *dst, size_t n, int kind, float a, float b, uint64_t seed, hipStream_t st);
-void launch_build_table(const int *ids, const float *w, int S, int k, int E, const TableOut &t, int tmax,
-                        hipStream_t st);
+void launch_build_table(const int *ids, int S, int k, int E, const TableOut &t, int tmax, hipStream_t st);
 }  // namespace phip

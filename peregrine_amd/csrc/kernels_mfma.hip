@@ -53,7 +53,7 @@ __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const i
     constexpr int BB = W4 ? 16 : 32;
     extern __shared__ float sxl[];   // EPI_B32: [nb][32] activation scales of this tile's rows
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int tile = blockIdx.y;
     if (tile >= a.plan.counts[1]) return;
     const int e = a.plan.mt_exp[tile], r0 = a.plan.mt_row0[tile], rend = a.plan.mt_rend[tile];
@@ -87,8 +87,9 @@ __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const i
         int o = GATEUP ? n0 + j : n0 + s * 32 + j;
         oc[s] = o;
         if (o >= g.Op) o = g.Op - 1;
-        wp[s] = a.desc[e].w[mat] + ((size_t)(o >> 6) * g.nb * TILE_O + (o & 63)) * BB + hh * (BB / 2);
-        sp[s] = a.desc[e].sc[mat] + (size_t)(o >> 6) * g.ng * TILE_O + (o & 63);
+        wp[s] = (const uint8_t *)gptr(a.desc[e].w[mat] + ((size_t)(o >> 6) * g.nb * TILE_O + (o & 63)) * BB +
+                                      hh * (BB / 2));
+        sp[s] = (const float *)gptr(a.desc[e].sc[mat] + (size_t)(o >> 6) * g.ng * TILE_O + (o & 63));
     }
 
     float acc[NSUB][16];
@@ -113,7 +114,7 @@ __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const i
 #pragma unroll
         for (int s = 0; s < NSUB; ++s) Bn[s] = load_b<W4>(wp[s] + (size_t)bn * TILE_O * BB);
 
-        const bool gend = ((b + 1) % g.gpb == 0) || (b + 1 == g.nb);
+        const bool gend = grp_end(b, g.gshift, g.nb);
 #pragma unroll
         for (int s = 0; s < NSUB; ++s) {
             const v16i cin = (EPI == EPI_B32) ? v16i{} : iacc[s];
@@ -132,7 +133,7 @@ __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const i
                 iacc[s] = d;
             } else if constexpr (EPI == EPI_GRP) {
                 if (gend) {
-                    const float sw = sp[s][(size_t)(b / g.gpb) * TILE_O];
+                    const float sw = sp[s][(size_t)grp_of(b, g.gshift) * TILE_O];
 #pragma unroll
                     for (int i = 0; i < 16; ++i) acc[s][i] = __fadd_rn(acc[s][i], __fmul_rn((float)d[i], sw));
                     iacc[s] = v16i{};
@@ -140,7 +141,7 @@ __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const i
                     iacc[s] = d;
                 }
             } else {
-                const float sw = sp[s][(size_t)(b / g.gpb) * TILE_O];
+                const float sw = sp[s][(size_t)grp_of(b, g.gshift) * TILE_O];
                 const float4 *sx4 = (const float4 *)(sxl + b * 32 + 4 * hh);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {

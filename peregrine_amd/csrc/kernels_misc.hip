@@ -12,44 +12,68 @@ namespace phip {
 // row. Output bytes go to the permuted device layout (perm8) and the row is
 // zero-padded to Kp, so padded weight columns contribute nothing.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
+__global__ __launch_bounds__(1024) void quant_rows_kernel(QuantArgs a) {
+    // ACT_ROW: one workgroup per row; every thread loads its elements in one
+    // round, then a block reduction gives the row's amax.
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *x = a.x + (size_t)row * a.x_stride;
     int8_t *q = a.q + (size_t)row * a.q_stride;
-    if (a.mode == ACT_ROW) {
-        __shared__ float red[4];
-        float m = 0.0f;
-        for (int k = tid; k < a.K; k += 256) m = fmaxf(m, fabsf(x[k]));
-        m = warp_max(m, 64);
-        if (lane == 0) red[wave] = m;
-        __syncthreads();
-        m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-        float s = __fdiv_rn(m, 127.0f);
-        if (s < 1e-12f) s = 1e-12f;
-        const float inv = __fdiv_rn(1.0f, s);
-        for (int k = tid; k < a.Kp; k += 256) {
-            float v = k < a.K ? rintf(__fmul_rn(x[k], inv)) : 0.0f;
-            q[perm8(k)] = (int8_t)(int)v;
-        }
-        if (tid == 0) a.s[(size_t)row * a.s_stride] = s;
-    } else {
-        const int half = lane >> 5, l32 = lane & 31, nb = a.Kp / BLK;
-        for (int b = wave * 2 + half; b < nb; b += 8) {
-            const int k = b * BLK + l32;
-            const float v = k < a.K ? x[k] : 0.0f;
-            float m = warp_max(fabsf(v), 32);
-            float s = __fdiv_rn(m, 127.0f);
-            if (s < 1e-12f) s = 1e-12f;
-            const float inv = __fdiv_rn(1.0f, s);
-            q[perm8(k)] = (int8_t)(int)rintf(__fmul_rn(v, inv));
-            if (l32 == 0) a.s[(size_t)row * a.s_stride + b] = s;
-        }
+    __shared__ float red[16];
+    constexpr int PER = 8;
+    float v[PER];
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int k = tid + j * 1024;
+        v[j] = k < a.K ? x[k] : 0.0f;
+        m = fmaxf(m, fabsf(v[j]));
     }
+    for (int k = tid + PER * 1024; k < a.K; k += 1024) m = fmaxf(m, fabsf(x[k]));
+    m = warp_max(m, 64);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = red[0];
+    for (int w = 1; w < 16; w++) m = fmaxf(m, red[w]);
+    float s = __fdiv_rn(m, 127.0f);
+    if (s < 1e-12f) s = 1e-12f;
+    const float inv = __fdiv_rn(1.0f, s);
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int k = tid + j * 1024;
+        if (k < a.Kp) q[perm8(k)] = (int8_t)(int)rintf(__fmul_rn(v[j], inv));
+    }
+    for (int k = tid + PER * 1024; k < a.Kp; k += 1024) {
+        const float xv = k < a.K ? x[k] : 0.0f;
+        q[perm8(k)] = (int8_t)(int)rintf(__fmul_rn(xv, inv));
+    }
+    if (tid == 0) a.s[(size_t)row * a.s_stride] = s;
+}
+
+__global__ __launch_bounds__(256) void quant_blocks_kernel(QuantArgs a) {
+    // ACT_B32: each 32-lane half-wave owns one 32-block; one load per thread.
+    const int row = blockIdx.y, tid = threadIdx.x;
+    const int b = blockIdx.x * 8 + (tid >> 5), l32 = tid & 31;
+    if (b * BLK >= a.Kp) return;
+    const float *x = a.x + (size_t)row * a.x_stride;
+    const int k = b * BLK + l32;
+    const float v = k < a.K ? x[k] : 0.0f;
+    const float m = warp_max(fabsf(v), 32);
+    float s = __fdiv_rn(m, 127.0f);
+    if (s < 1e-12f) s = 1e-12f;
+    const float inv = __fdiv_rn(1.0f, s);
+    a.q[(size_t)row * a.q_stride + perm8(k)] = (int8_t)(int)rintf(__fmul_rn(v, inv));
+    if (l32 == 0) a.s[(size_t)row * a.s_stride + b] = s;
 }
 
 void launch_quant_rows(const QuantArgs &a, hipStream_t st) {
     if (a.rows <= 0) return;
-    hipLaunchKernelGGL(quant_rows_kernel, dim3(a.rows), dim3(256), 0, st, a);
+    if (a.mode == ACT_ROW) {
+        hipLaunchKernelGGL(quant_rows_kernel, dim3(a.rows), dim3(1024), 0, st, a);
+    } else {
+        const int nb = a.Kp / BLK;
+        hipLaunchKernelGGL(quant_blocks_kernel, dim3((unsigned)((nb + 7) / 8), (unsigned)a.rows), dim3(256), 0, st,
+                           a);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -118,25 +142,34 @@ void launch_repack(const uint8_t *raw, const float *raw_sc, int fmt, int I, int 
 // add, no atomics. CSR form (row_ptr != null) or the device table's padded
 // form (row_ptr == null: k slots per token, -1 terminates).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void combine_kernel(float *out, const float *y, const int *row_ptr,
-                                                      const int *row_idx, const float *rw, int D, int y_stride,
-                                                      int k) {
+__global__ __launch_bounds__(256) void combine_csr_kernel(float *out, const float *y, const int *row_ptr,
+                                                          const int *row_idx, const float *rw, int D, int y_stride) {
     const int s = blockIdx.y;
     const int d = blockIdx.x * 256 + threadIdx.x;
     if (d >= D) return;
-    int lo, hi;
-    if (row_ptr) {
-        lo = row_ptr[s];
-        hi = row_ptr[s + 1];
-    } else {
-        lo = s * k;
-        hi = lo + k;
-    }
     float acc = 0.0f;
-    for (int j = lo; j < hi; j++) {
+    for (int j = row_ptr[s]; j < row_ptr[s + 1]; j++) {
         const int r = row_idx[j];
-        if (r < 0) break;
         acc = __fadd_rn(acc, __fmul_rn(rw[r], y[(size_t)r * y_stride + d]));
+    }
+    out[(size_t)s * D + d] = acc;
+}
+
+// Device-table form: token s adds its rows tok_rows[s*k + j] (union order,
+// -1 terminates) weighted by w[s*k + tok_kk[s*k + j]] — the reference scatter
+// out[s] += w * y (mlp.rs:111-119) from a zero row.
+__global__ __launch_bounds__(256) void combine_tok_kernel(float *out, const float *y, const int *tok_rows,
+                                                          const int *tok_kk, const float *w, int k, int D,
+                                                          int y_stride) {
+    const int s = blockIdx.y;
+    const int d = blockIdx.x * 256 + threadIdx.x;
+    if (d >= D) return;
+    float acc = 0.0f;
+    for (int j = 0; j < k; j++) {
+        const int r = tok_rows ? tok_rows[(size_t)s * k + j] : j;
+        if (r < 0) break;
+        const float wt = w[(size_t)s * k + (tok_kk ? tok_kk[(size_t)s * k + j] : j)];
+        acc = __fadd_rn(acc, __fmul_rn(wt, y[(size_t)r * y_stride + d]));
     }
     out[(size_t)s * D + d] = acc;
 }
@@ -144,15 +177,15 @@ __global__ __launch_bounds__(256) void combine_kernel(float *out, const float *y
 void launch_combine(float *out, const float *y, const int *row_ptr, const int *row_idx, const float *rw, int s_n,
                     int D, int y_stride, hipStream_t st) {
     if (s_n <= 0) return;
-    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((D + 255) / 256), (unsigned)s_n), dim3(256), 0, st, out, y,
-                       row_ptr, row_idx, rw, D, y_stride, 0);
+    hipLaunchKernelGGL(combine_csr_kernel, dim3((unsigned)((D + 255) / 256), (unsigned)s_n), dim3(256), 0, st, out,
+                       y, row_ptr, row_idx, rw, D, y_stride);
 }
 
-void launch_combine_padded(float *out, const float *y, const int *tok_rows, const float *rw, int s_n, int k, int D,
-                           int y_stride, hipStream_t st) {
+void launch_combine_tok(float *out, const float *y, const int *tok_rows, const int *tok_kk, const float *w, int s_n,
+                        int k, int D, int y_stride, hipStream_t st) {
     if (s_n <= 0) return;
-    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((D + 255) / 256), (unsigned)s_n), dim3(256), 0, st, out, y,
-                       (const int *)nullptr, tok_rows, rw, D, y_stride, k);
+    hipLaunchKernelGGL(combine_tok_kernel, dim3((unsigned)((D + 255) / 256), (unsigned)s_n), dim3(256), 0, st, out,
+                       y, tok_rows, tok_kk, w, k, D, y_stride);
 }
 
 // ---------------------------------------------------------------------------
@@ -161,54 +194,161 @@ void launch_combine_padded(float *out, const float *y, const int *tok_rows, cons
 // then w_j = exp(l_j - l_0) / sum_j exp(l_j - l_0) summed in selection order.
 // One wavefront per token.
 // ---------------------------------------------------------------------------
+// One wavefront routes one token. Top-k by rank: element e's rank is the
+// number of valid logits that beat it (greater, or equal with a lower index);
+// NaN and -inf never qualify, exactly as the strict `>` scan of the greedy loop
+// (router.rs:97-118) never picks them. The k lowest ranks are the greedy
+// selection in order. lv: LDS scratch of E floats (E <= 1024); selv/seli: 16.
+// desc/row_desc (optional): copy the chosen experts' descriptors per slot.
+template <int PER>
+__device__ void route_token(const float *l, int E, int k, int *ids, float *w, float *lv, float *selv, int *seli,
+                            const ExpertDesc *desc, ExpertDesc *row_desc) {
+    const int lane = threadIdx.x & 63;
+    for (int e = lane; e < E; e += 64) lv[e] = l[e];
+    __builtin_amdgcn_wave_barrier();   // one wavefront: LDS ops complete in order
+    float ve[PER];
+    int rank[PER];
+    bool valid[PER];
+    int nvalid = 0;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int e = lane + 64 * j;
+        ve[j] = e < E ? lv[e] : -INFINITY;
+        valid[j] = ve[j] > -INFINITY;   // false for NaN, -inf and padding
+        nvalid += valid[j];
+        rank[j] = 0;
+    }
+    // every lane streams all E logits (broadcast LDS reads, 16 at a time)
+    for (int e0 = 0; e0 < E; e0 += 16) {
+        float v2[16];
+#pragma unroll
+        for (int q = 0; q < 16; q++) v2[q] = e0 + q < E ? lv[e0 + q] : -INFINITY;
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+            const int e2 = e0 + q;
+#pragma unroll
+            for (int j = 0; j < PER; j++) {
+                const int e = lane + 64 * j;
+                rank[j] += (v2[q] > ve[j]) | ((v2[q] == ve[j]) & (e2 < e));
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        if (valid[j] && rank[j] < k) {
+            selv[rank[j]] = ve[j];
+            seli[rank[j]] = lane + 64 * j;
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) nvalid += __shfl_xor(nvalid, off);
+    __builtin_amdgcn_wave_barrier();
+    const int kept = nvalid < k ? nvalid : k;
+    const float myex = lane < kept ? exp_cr(__fsub_rn(selv[lane], selv[0])) : 0.0f;
+    float z = 0.0f;
+    for (int kk = 0; kk < kept; kk++) z = __fadd_rn(z, __shfl(myex, kk));
+    if (lane < k) {
+        const bool ok = lane < kept;
+        const int id = ok ? seli[lane] : 0;
+        ids[lane] = id;
+        w[lane] = ok ? __fdiv_rn(myex, z) : 0.0f;
+        if (row_desc) row_desc[lane] = desc[id];
+    }
+}
+
+template <int PER>
 __global__ __launch_bounds__(64) void route_softmax_kernel(const float *logits, int E, int k, int *ids, float *w) {
-    const int s = blockIdx.x, lane = threadIdx.x;
-    const float *l = logits + (size_t)s * E;
-    int sel[16];
-    int kept = k;
-    for (int kk = 0; kk < k; kk++) {
-        float bv = -INFINITY;
-        int be = -1;
-        for (int e = lane; e < E; e += 64) {
-            bool taken = false;
-            for (int j = 0; j < kk; j++) taken |= (sel[j] == e);
-            const float v = l[e];
-            if (!taken && v > bv) {
-                bv = v;
-                be = e;
-            }
+    __shared__ float lv[1024], selv[16];
+    __shared__ int seli[16];
+    const int s = blockIdx.x;
+    route_token<PER>(logits + (size_t)s * E, E, k, ids + (size_t)s * k, w + (size_t)s * k, lv, selv, seli, nullptr,
+                     nullptr);
+}
+
+// Router fused with the activation quantisation of the same token. Grid
+// (S, quant slabs): workgroup (s, 0) routes token s with its first wave; every
+// workgroup quantises its slab of token s (ACT_B32: 8 blocks, one element per
+// thread; ACT_ROW: one slab holds the whole row). Same arithmetic as
+// quant_rows_kernel / quant_blocks_kernel.
+template <int PER>
+__global__ __launch_bounds__(256) void route_quant_kernel(const float *logits, int E, int k, int *ids, float *w,
+                                                          QuantArgs a, const ExpertDesc *desc,
+                                                          ExpertDesc *row_desc) {
+    __shared__ float lv[1024], selv[16], red[4];
+    __shared__ int seli[16];
+    const int s = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    if (blockIdx.y == 0 && wave == 0)
+        route_token<PER>(logits + (size_t)s * E, E, k, ids + (size_t)s * k, w + (size_t)s * k, lv, selv, seli, desc,
+                         row_desc ? row_desc + (size_t)s * k : nullptr);
+    const float *x = a.x + (size_t)s * a.x_stride;
+    int8_t *q = a.q + (size_t)s * a.q_stride;
+    if (a.mode == ACT_B32) {
+        const int b = blockIdx.y * 8 + (tid >> 5), l32 = tid & 31;
+        if (b * BLK >= a.Kp) return;
+        const int kx = b * BLK + l32;
+        const float v = kx < a.K ? x[kx] : 0.0f;
+        const float m = warp_max(fabsf(v), 32);
+        float sc = __fdiv_rn(m, 127.0f);
+        if (sc < 1e-12f) sc = 1e-12f;
+        const float inv = __fdiv_rn(1.0f, sc);
+        q[perm8(kx)] = (int8_t)(int)rintf(__fmul_rn(v, inv));
+        if (l32 == 0) a.s[(size_t)s * a.s_stride + b] = sc;
+    } else {
+        constexpr int PX = 32;   // K <= 8192 from registers, the rest re-read
+        float v[PX];
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < PX; j++) {
+            const int kx = tid + 256 * j;
+            v[j] = kx < a.K ? x[kx] : 0.0f;
+            m = fmaxf(m, fabsf(v[j]));
         }
-        for (int off = 32; off > 0; off >>= 1) {
-            const float ov = __shfl_xor(bv, off);
-            const int oe = __shfl_xor(be, off);
-            if (oe >= 0 && (be < 0 || ov > bv || (ov == bv && oe < be))) {
-                bv = ov;
-                be = oe;
-            }
+        for (int kx = tid + 256 * PX; kx < a.K; kx += 256) m = fmaxf(m, fabsf(x[kx]));
+        m = warp_max(m, 64);
+        if (lane == 0) red[tid >> 6] = m;
+        __syncthreads();
+        m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        float sc = __fdiv_rn(m, 127.0f);
+        if (sc < 1e-12f) sc = 1e-12f;
+        const float inv = __fdiv_rn(1.0f, sc);
+#pragma unroll
+        for (int j = 0; j < PX; j++) {
+            const int kx = tid + 256 * j;
+            if (kx < a.Kp) q[perm8(kx)] = (int8_t)(int)rintf(__fmul_rn(v[j], inv));
         }
-        if (be < 0) {
-            kept = kk;
-            break;
+        for (int kx = tid + 256 * PX; kx < a.Kp; kx += 256) {
+            const float xv = kx < a.K ? x[kx] : 0.0f;
+            q[perm8(kx)] = (int8_t)(int)rintf(__fmul_rn(xv, inv));
         }
-        sel[kk] = be;
+        if (tid == 0) a.s[(size_t)s * a.s_stride] = sc;
     }
-    if (lane == 0) {
-        float ex[16];
-        float z = 0.0f;
-        for (int kk = 0; kk < kept; kk++) {
-            ex[kk] = exp_cr(__fsub_rn(l[sel[kk]], l[sel[0]]));
-            z = __fadd_rn(z, ex[kk]);
-        }
-        for (int kk = 0; kk < k; kk++) {
-            ids[(size_t)s * k + kk] = kk < kept ? sel[kk] : 0;
-            w[(size_t)s * k + kk] = kk < kept ? __fdiv_rn(ex[kk], z) : 0.0f;
-        }
-    }
+}
+
+template <int PER>
+static void route_quant_t(const float *logits, int S, int E, int k, int *ids, float *w, const QuantArgs &a,
+                          const ExpertDesc *desc, ExpertDesc *row_desc, hipStream_t st) {
+    const int slabs = a.mode == ACT_B32 ? (a.Kp / BLK + 7) / 8 : 1;
+    hipLaunchKernelGGL(route_quant_kernel<PER>, dim3((unsigned)S, (unsigned)slabs), dim3(256), 0, st, logits, E, k,
+                       ids, w, a, desc, row_desc);
+}
+
+void launch_route_quant(const float *logits, int S, int E, int k, int *ids, float *w, const QuantArgs &a,
+                        const ExpertDesc *desc, ExpertDesc *row_desc, hipStream_t st) {
+    if (S <= 0) return;
+    if (E <= 64) route_quant_t<1>(logits, S, E, k, ids, w, a, desc, row_desc, st);
+    else if (E <= 128) route_quant_t<2>(logits, S, E, k, ids, w, a, desc, row_desc, st);
+    else if (E <= 256) route_quant_t<4>(logits, S, E, k, ids, w, a, desc, row_desc, st);
+    else if (E <= 512) route_quant_t<8>(logits, S, E, k, ids, w, a, desc, row_desc, st);
+    else route_quant_t<16>(logits, S, E, k, ids, w, a, desc, row_desc, st);
 }
 
 void launch_route_softmax(const float *logits, int S, int E, int k, int *ids, float *w, hipStream_t st) {
     if (S <= 0) return;
-    hipLaunchKernelGGL(route_softmax_kernel, dim3((unsigned)S), dim3(64), 0, st, logits, E, k, ids, w);
+    const dim3 g((unsigned)S), b(64);
+    if (E <= 64) hipLaunchKernelGGL(route_softmax_kernel<1>, g, b, 0, st, logits, E, k, ids, w);
+    else if (E <= 128) hipLaunchKernelGGL(route_softmax_kernel<2>, g, b, 0, st, logits, E, k, ids, w);
+    else if (E <= 256) hipLaunchKernelGGL(route_softmax_kernel<4>, g, b, 0, st, logits, E, k, ids, w);
+    else if (E <= 512) hipLaunchKernelGGL(route_softmax_kernel<8>, g, b, 0, st, logits, E, k, ids, w);
+    else hipLaunchKernelGGL(route_softmax_kernel<16>, g, b, 0, st, logits, E, k, ids, w);
 }
 
 // ---------------------------------------------------------------------------
@@ -219,130 +359,180 @@ void launch_route_softmax(const float *logits, int S, int E, int k, int *ids, fl
 //   contributions listed in union order (the order the scatter adds them).
 // Also emits the 32-row M-tile list the MFMA arm walks. One workgroup; every
 // step is a counting pass, so the result does not depend on thread timing.
-// Limits: E <= 1024, k <= 16.
+// The router ids are staged in LDS once; nothing written is read back.
+// Limits: E <= 512, k <= 16 (ids beyond TBL_MAXN are read from global).
 // ---------------------------------------------------------------------------
-constexpr int TBL_MAXE = 1024;
+// Exclusive scan of one int per thread across a workgroup of up to 1024
+// threads (wave scans, then a scan of the wave totals). Ends synchronised.
+__device__ int block_exclusive_scan(int v, int *tmp) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+    int inc = v;
+    for (int off = 1; off < 64; off <<= 1) {
+        const int o = __shfl_up(inc, off);
+        if (lane >= off) inc += o;
+    }
+    __syncthreads();
+    if (lane == 63) tmp[wave] = inc;
+    __syncthreads();
+    int wbase = 0;
+    for (int w = 0; w < wave; w++) wbase += tmp[w];
+    (void)nw;
+    __syncthreads();
+    return wbase + inc - v;
+}
 
-__global__ __launch_bounds__(1024) void build_table_kernel(const int *ids, const float *wts, int S, int k, int E,
-                                                           TableOut t, int tmax) {
+constexpr int TBL_MAXE = 512;
+constexpr int TBL_MAXN = 16384;
+
+__global__ __launch_bounds__(1024) void build_table_kernel(const int *ids, int S, int k, int E, TableOut t,
+                                                           int tmax) {
+    __shared__ short sid[TBL_MAXN];
     __shared__ int first[TBL_MAXE], cnt[TBL_MAXE], rank[TBL_MAXE], fill[TBL_MAXE], uex[TBL_MAXE];
     __shared__ unsigned long long mask[TBL_MAXE];
-    __shared__ int s_nu;
+    __shared__ int cpos[1024];
+    __shared__ int scan_tmp[32];
+    __shared__ int s_nu, s_carry[2];
     const int tid = threadIdx.x, nth = blockDim.x;
     const int N = S * k;
+    const bool in_lds = N <= TBL_MAXN;
+    auto id_at = [&](int i) -> int {
+        const int e = in_lds ? (int)sid[i] : ids[i];
+        return (e >= 0 && e < E) ? e : -1;
+    };
+    if (in_lds)
+        for (int i = tid; i < N; i += nth) sid[i] = (short)max(-1, min(ids[i], 32767));
     for (int e = tid; e < E; e += nth) {
         first[e] = INT_MAX;
         cnt[e] = 0;
         mask[e] = 0ull;
+        rank[e] = -1;
     }
-    if (tid == 0) s_nu = 0;
     __syncthreads();
     for (int i = tid; i < N; i += nth) {
-        const int e = ids[i];
-        if (e >= 0 && e < E) {
+        const int e = id_at(i);
+        if (e >= 0) {
             atomicMin(&first[e], i);
             atomicAdd(&cnt[e], 1);
         }
     }
     __syncthreads();
-    for (int e = tid; e < E; e += nth) {
-        int r = -1;
-        if (cnt[e] > 0) {
-            r = 0;
-            for (int e2 = 0; e2 < E; e2++) r += (cnt[e2] > 0 && first[e2] < first[e]);
-            atomicAdd(&s_nu, 1);
+    // union rank = number of first occurrences before an expert's first
+    // occurrence: flag first occurrences, then one block-wide scan over the
+    // positions (each thread owns a contiguous run of them)
+    {
+        const int per = (N + nth - 1) / nth;
+        const int lo = min(N, tid * per), hi = min(N, lo + per);
+        int nf = 0;
+        for (int i = lo; i < hi; i++) {
+            const int e = id_at(i);
+            nf += (e >= 0 && first[e] == i);
         }
-        rank[e] = r;
+        int base = block_exclusive_scan(nf, scan_tmp);
+        for (int i = lo; i < hi; i++) {
+            const int e = id_at(i);
+            if (e >= 0 && first[e] == i) {
+                rank[e] = base;
+                uex[base] = e;
+                base++;
+            }
+        }
+        if (tid == nth - 1) s_nu = base;
     }
     __syncthreads();
-    for (int e = tid; e < E; e += nth)
-        if (rank[e] >= 0) uex[rank[e]] = e;
-    __syncthreads();
     const int n_u = s_nu;
-    for (int u = tid; u < n_u; u += nth) {
-        int off = 0, mt = 0;
-        for (int v = 0; v < u; v++) {
-            const int c = cnt[uex[v]];
-            off += c;
-            mt += (c + 31) / 32;
+    // row offsets and M-tile offsets in union order (block scans over experts)
+    for (int u0 = 0; u0 < n_u; u0 += nth) {
+        const int u = u0 + tid;
+        const int c = u < n_u ? cnt[uex[u]] : 0;
+        const int off = block_exclusive_scan(c, scan_tmp) + (u0 ? s_carry[0] : 0);
+        const int mt = block_exclusive_scan((c + 31) / 32, scan_tmp) + (u0 ? s_carry[1] : 0);
+        if (u < n_u) {
+            const int e = uex[u];
+            fill[e] = off;
+            t.uexp[u] = e;
+            t.off[u] = off;
+            for (int j = 0; j < (c + 31) / 32 && mt + j < tmax; j++) {
+                t.mt_exp[mt + j] = e;
+                t.mt_row0[mt + j] = off + 32 * j;
+                t.mt_rend[mt + j] = off + c;
+            }
+            if (u == n_u - 1) {
+                t.off[n_u] = off + c;
+                t.hdr[0] = off + c;
+                t.hdr[1] = mt + (c + 31) / 32;
+                t.hdr[2] = n_u;
+                t.hdr[3] = 0;
+            }
         }
-        const int e = uex[u], c = cnt[e];
-        fill[e] = off;
-        t.uexp[u] = e;
-        t.off[u] = off;
-        for (int j = 0; j < (c + 31) / 32 && mt + j < tmax; j++) {
-            t.mt_exp[mt + j] = e;
-            t.mt_row0[mt + j] = off + 32 * j;
-            t.mt_rend[mt + j] = off + c;
+        __syncthreads();
+        if (tid == nth - 1) {
+            s_carry[0] = off + c;
+            s_carry[1] = mt + (c + 31) / 32;
         }
-        if (u == n_u - 1) {
-            t.off[n_u] = off + c;
-            t.hdr[0] = off + c;
-            t.hdr[1] = mt + (c + 31) / 32;
-            t.hdr[2] = n_u;
-            t.hdr[3] = 0;
-        }
+        __syncthreads();
     }
     if (n_u == 0 && tid == 0) {
         t.off[0] = 0;
-        t.hdr[0] = 0;
-        t.hdr[1] = 0;
-        t.hdr[2] = 0;
-        t.hdr[3] = 0;
+        t.hdr[0] = t.hdr[1] = t.hdr[2] = t.hdr[3] = 0;
     }
     __syncthreads();
-    // stable placement, 64 tokens per pass: rank within the pass = earlier
-    // tokens of the pass that chose the same expert (a popcount of a bitmask)
+    // stable placement, 64 tokens per pass: the rank of an entry among its
+    // expert's rows in this pass = earlier tokens of the pass with the same
+    // expert (a popcount of a per-expert token bitmask)
     for (int c0 = 0; c0 < S; c0 += 64) {
         const int i = c0 * k + tid;
         const bool mine = tid < 64 * k && i < N;
         int e = -1, bit = 0;
         if (mine) {
-            e = ids[i];
+            e = id_at(i);
             bit = i / k - c0;
-            if (e >= 0 && e < E) atomicOr(&mask[e], 1ull << bit);
-            else e = -1;
+            if (e >= 0) atomicOr(&mask[e], 1ull << bit);
         }
         __syncthreads();
-        if (e >= 0) {
-            const int r = fill[e] + __popcll(mask[e] & ((1ull << bit) - 1ull));
-            t.row_tok[r] = i / k;
-            t.row_kk[r] = i % k;
-            t.row_exp[r] = e;
-            t.rw_row[r] = wts[i];
-            t.tok_rows[i] = r;
-        } else if (mine) {
-            t.tok_rows[i] = -1;
+        if (mine) {
+            int r = -1;
+            if (e >= 0) {
+                r = fill[e] + __popcll(mask[e] & ((1ull << bit) - 1ull));
+                t.row_tok[r] = i / k;
+                t.row_kk[r] = i % k;
+                t.row_exp[r] = e;
+            }
+            cpos[tid] = r;
         }
         __syncthreads();
         for (int e2 = tid; e2 < E; e2 += nth) {
             fill[e2] += __popcll(mask[e2]);
             mask[e2] = 0ull;
         }
-        __syncthreads();
-    }
-    // each token's rows, sorted by union rank (insertion sort, k <= 16)
-    for (int s = tid; s < S; s += nth) {
-        int rr[16], rk[16], j = 0;
-        for (int kk = 0; kk < k; kk++) {
-            const int r = t.tok_rows[(size_t)s * k + kk];
-            if (r < 0) continue;
-            rr[j] = r;
-            rk[j] = rank[ids[(size_t)s * k + kk]];
-            j++;
-        }
-        for (int a = 1; a < j; a++)
-            for (int b = a; b > 0 && rk[b - 1] > rk[b]; b--) {
-                int tmp = rk[b]; rk[b] = rk[b - 1]; rk[b - 1] = tmp;
-                tmp = rr[b]; rr[b] = rr[b - 1]; rr[b - 1] = tmp;
+        // this pass's tokens: rows sorted by union rank (insertion sort, k <= 16)
+        const int s = c0 + tid;
+        if (tid < 64 && s < S) {
+            int rr[16], rk[16], kq[16], j = 0;
+            for (int kk = 0; kk < k; kk++) {
+                const int r = cpos[tid * k + kk];
+                if (r < 0) continue;
+                rr[j] = r;
+                kq[j] = kk;
+                rk[j] = rank[id_at(s * k + kk)];
+                j++;
             }
-        for (int a = 0; a < k; a++) t.tok_rows[(size_t)s * k + a] = a < j ? rr[a] : -1;
+            for (int a = 1; a < j; a++)
+                for (int b = a; b > 0 && rk[b - 1] > rk[b]; b--) {
+                    int tmp = rk[b]; rk[b] = rk[b - 1]; rk[b - 1] = tmp;
+                    tmp = rr[b]; rr[b] = rr[b - 1]; rr[b - 1] = tmp;
+                    tmp = kq[b]; kq[b] = kq[b - 1]; kq[b - 1] = tmp;
+                }
+            for (int a = 0; a < k; a++) {
+                t.tok_rows[(size_t)s * k + a] = a < j ? rr[a] : -1;
+                t.tok_kk[(size_t)s * k + a] = a < j ? kq[a] : 0;
+            }
+        }
+        __syncthreads();
     }
 }
 
-void launch_build_table(const int *ids, const float *w, int S, int k, int E, const TableOut &t, int tmax,
-                        hipStream_t st) {
-    hipLaunchKernelGGL(build_table_kernel, dim3(1), dim3(1024), 0, st, ids, w, S, k, E, t, tmax);
+void launch_build_table(const int *ids, int S, int k, int E, const TableOut &t, int tmax, hipStream_t st) {
+    hipLaunchKernelGGL(build_table_kernel, dim3(1), dim3(1024), 0, st, ids, S, k, E, t, tmax);
 }
 
 // ---------------------------------------------------------------------------

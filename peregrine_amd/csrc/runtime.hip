@@ -34,6 +34,7 @@ struct ColiHipExpertSet {
     int device, count;
     MatGeom gg, gd;          // gate/up geometry, down geometry
     ExpertDesc *desc_dev;    // [count]
+    int buf_ok;              // gate/up pairs fit one 4 GB buffer window
 };
 
 namespace {
@@ -51,7 +52,7 @@ struct Ctx {
     hipStream_t stream = nullptr;
     size_t tensor_count = 0, tensor_bytes = 0;
     unsigned gen = 0;   // bumped on every scratch reallocation
-    Buf xq, sx, h, hq, sh, y, red_out, meta, tbl;
+    Buf xq, sx, h, hq, sh, y, red_out, meta, tbl, rdesc;
     Buf pin_x, pin_y, pin_meta;
     hipEvent_t ev[N_EVENTS] = {};
     hipEvent_t user_ev[16] = {};
@@ -72,6 +73,7 @@ int g_act_group = -1;   // -1: read COLI_HIP_ACT_GROUP on first use
 int g_arm = -2;         // -2: read COLI_HIP_ARM on first use
 int g_profile = -1;
 int32_t *g_dbg_gu = nullptr, *g_dbg_dn = nullptr;
+long long *g_trace_gu = nullptr, *g_trace_dn = nullptr;
 thread_local int g_cur_dev = -1;
 
 int hip_ok(hipError_t e, const char *what) {
@@ -151,7 +153,7 @@ int reserve_pinned(Ctx *c, Buf &b, size_t bytes) {
 }
 
 void free_ctx(Ctx *c) {
-    Buf *dev[] = {&c->xq, &c->sx, &c->h, &c->hq, &c->sh, &c->y, &c->red_out, &c->meta, &c->tbl};
+    Buf *dev[] = {&c->xq, &c->sx, &c->h, &c->hq, &c->sh, &c->y, &c->red_out, &c->meta, &c->tbl, &c->rdesc};
     for (Buf *b : dev) {
         if (b->p) hipFree(b->p);
         *b = Buf{};
@@ -197,6 +199,7 @@ int make_geom(int fmt, int I, int O, int gs, MatGeom *g) {
     g->per_row = grouped ? 0 : 1;
     g->gpb = grouped ? gs / 32 : g->nb;
     g->ng = grouped ? (g->nb + g->gpb - 1) / g->gpb : 1;
+    g->gshift = grouped ? __builtin_ctz((unsigned)g->gpb) : 30;
     return 1;
 }
 
@@ -271,6 +274,24 @@ int upload_impl(ColiHipTensor **tensor, const void *weights, const float *scales
 }
 
 int epi_act(int ga) { return ga == 32 ? ACT_B32 : ACT_ROW; }
+
+// Whether the gate and up tensors of one expert can be addressed from a
+// single buffer descriptor (distance + size below 2 GB, for weights and scales).
+bool pair_in_window(const ColiHipTensor *g, const ColiHipTensor *u) {
+    const auto span = [](const void *a, const void *b, size_t n) {
+        const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+        return (x > y ? x - y : y - x) + n;
+    };
+    const size_t lim = (size_t)1 << 31;
+    return span(g->w, u->w, std::max(g->w_bytes, u->w_bytes)) < lim &&
+           span(g->sc, u->sc, std::max(g->sc_bytes, u->sc_bytes)) < lim;
+}
+
+int group_buf_ok(ColiHipTensor *const *gates, ColiHipTensor *const *ups, int count) {
+    for (int c = 0; c < count; c++)
+        if (!pair_in_window(gates[c], ups[c])) return 0;
+    return 1;
+}
 
 // Validate a gate/up/down triple list; fills the two geometries.
 int check_group(ColiHipTensor *const *gates, ColiHipTensor *const *ups, ColiHipTensor *const *downs, int count,
@@ -360,15 +381,25 @@ int reserve_rows(Ctx *c, const MatGeom &gg, const MatGeom &gd, int rows_x, int R
     return 1;
 }
 
+// Optional pieces of a dispatch beyond the expert matmuls.
+struct DispatchOpts {
+    bool x_quantized = false;   // xq/sx already written (fused router + quant)
+    bool act_zero = false;      // every row reads activation row 0 (one token)
+    int buf_ok = 0;             // gate/up pairs fit one buffer descriptor
+    int n_rows_fixed = -1;      // row count known on the host
+};
+
 // The kernel sequence of one dispatch after the activations are on the
 // device: quantise x, gate/up (+SwiGLU), [quantise h], down.
 void run_experts(Ctx *c, Prof &prof, const ExpertDesc *desc, const RowPlan &plan, const MatGeom &gg,
                  const MatGeom &gd, const float *x_dev, int rows_x, bool x_identity, int R_bound, int T_bound,
-                 int ga, int arm, const Scratch &s) {
+                 int ga, int arm, const Scratch &s, const DispatchOpts &opt = DispatchOpts()) {
     const int act = epi_act(ga);
-    QuantArgs qa{x_dev, gg.K, rows_x, gg.K, gg.Kp, s.xq, s.xs, s.sx, s.sxs, act};
-    prof.mark(COLI_HIP_K_QUANT_X);
-    launch_quant_rows(qa, c->stream);
+    if (!opt.x_quantized) {
+        QuantArgs qa{x_dev, gg.K, rows_x, gg.K, gg.Kp, s.xq, s.xs, s.sx, s.sxs, act};
+        prof.mark(COLI_HIP_K_QUANT_X);
+        launch_quant_rows(qa, c->stream);
+    }
 
     DotArgs da{};
     da.desc = desc;
@@ -384,7 +415,11 @@ void run_experts(Ctx *c, Prof &prof, const ExpertDesc *desc, const RowPlan &plan
     da.sh = s.sh;
     da.sh_stride = s.shs;
     da.dots = g_dbg_gu;
+    da.trace = g_trace_gu;
     da.act_identity = x_identity ? 1 : 0;
+    da.act_zero = opt.act_zero ? 1 : 0;
+    da.n_rows_fixed = opt.n_rows_fixed;
+    da.buf_ok = opt.buf_ok;
     prof.mark(COLI_HIP_K_GATEUP);
     if (arm == COLI_HIP_ARM_GEMV)
         launch_gemv_gateup(da, gg, act, R_bound, c->stream);
@@ -407,12 +442,15 @@ void run_experts(Ctx *c, Prof &prof, const ExpertDesc *desc, const RowPlan &plan
     dd.hq = nullptr;
     dd.sh = nullptr;
     dd.dots = g_dbg_dn;
+    dd.trace = g_trace_dn;
     dd.act_identity = 1;
+    dd.act_zero = 0;
     prof.mark(COLI_HIP_K_DOWN);
-    if (arm == COLI_HIP_ARM_GEMV)
+    if (arm == COLI_HIP_ARM_GEMV) {
         launch_gemv_down(dd, gd, act, R_bound, c->stream);
-    else
+    } else {
         launch_mfma_down(dd, gd, act, T_bound, c->stream);
+    }
 }
 
 struct ReduceSpec {
@@ -517,7 +555,9 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
     plan.mt_row0 = di + total + T;
     plan.mt_rend = di + total + 2 * T;
     plan.counts = di + total + 3 * T;
-    run_experts(c, prof, (const ExpertDesc *)dm, plan, gg, gd, x_dev, total, true, total, T, ga, arm, s);
+    DispatchOpts opt;
+    opt.buf_ok = group_buf_ok(gates, ups, count);
+    run_experts(c, prof, (const ExpertDesc *)dm, plan, gg, gd, x_dev, total, true, total, T, ga, arm, s, opt);
     float *res = s.y;
     if (red) {
         const int *drp = plan.counts + 2, *dri = drp + s_n + 1;
@@ -577,8 +617,11 @@ int coli_hip_init(const int *devices, int count) {
             return 0;
         }
         g_nctx++;
-        std::fprintf(stderr, "[HIP] device %d: %s (%s), %.1f GB HBM, %d CUs\n", device, prop.name, prop.gcnArchName,
-                     prop.totalGlobalMem / 1e9, prop.multiProcessorCount);
+        int lds = 0;
+        if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device) != hipSuccess) lds = 0;
+        set_lds_limit(lds);
+        std::fprintf(stderr, "[HIP] device %d: %s (%s), %.1f GB HBM, %d CUs, %d KB LDS per workgroup\n", device,
+                     prop.name, prop.gcnArchName, prop.totalGlobalMem / 1e9, prop.multiProcessorCount, lds / 1024);
     }
     return 1;
 }
@@ -844,6 +887,12 @@ void coli_hip_reset_stats(void) {
     }
 }
 
+int coli_hip_set_debug_trace(long long *gateup_dev, long long *down_dev) {
+    g_trace_gu = gateup_dev;
+    g_trace_dn = down_dev;
+    return 1;
+}
+
 int coli_hip_set_debug_dots(int32_t *gateup_dev, int32_t *down_dev) {
     g_dbg_gu = gateup_dev;
     g_dbg_dn = down_dev;
@@ -873,6 +922,7 @@ int coli_hip_expert_set_create(ColiHipExpertSet **set, ColiHipTensor *const *gat
     s->count = count;
     s->gg = gg;
     s->gd = gd;
+    s->buf_ok = group_buf_ok(gates, ups, count);
     if (!hip_ok(hipMalloc(&s->desc_dev, sizeof(ExpertDesc) * count), "expert set allocation") ||
         !hip_ok(hipMemcpy(s->desc_dev, hd.data(), sizeof(ExpertDesc) * count, hipMemcpyHostToDevice),
                 "expert set upload")) {
@@ -895,16 +945,22 @@ void coli_hip_expert_set_free(ColiHipExpertSet *s) {
 int coli_hip_route_softmax_topk_dev(int device, const float *logits_dev, int S, int E, int k, int *ids_dev,
                                     float *w_dev) {
     Ctx *c = find_ctx(device);
-    if (!logits_dev || !ids_dev || !w_dev || S < 1 || E < 1 || k < 1 || k > 16 || k > E || !select_ctx(c)) return 0;
+    if (!logits_dev || !ids_dev || !w_dev || S < 1 || E < 1 || E > 1024 || k < 1 || k > 16 || k > E || !select_ctx(c))
+        return 0;
     launch_route_softmax(logits_dev, S, E, k, ids_dev, w_dev, c->stream);
     return hip_ok(hipGetLastError(), "router launch");
 }
 
-int coli_hip_moe_forward_dev(const ColiHipExpertSet *set, const float *x_dev, int S, const int *ids_dev,
-                             const float *w_dev, int k, float *out_dev, int ga, int arm) {
+}  // extern "C"
+
+namespace {
+
+int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, const float *logits_dev, int *ids_dev,
+                     float *w_dev, int k, float *out_dev, int ga, int arm) {
     if (!set || !x_dev || !ids_dev || !w_dev || !out_dev || S < 1 || k < 1) return 0;
     if (k > 16) return fail("moe_forward: k > 16 is not supported");
-    if (set->count > 1024) return fail("moe_forward: more than 1024 experts");
+    if (set->count > 512) return fail("moe_forward: more than 512 experts");
+    if (logits_dev && k > set->count) return fail("moe_forward: k > experts");
     if (ga != 0 && ga != 32) return fail("moe_forward: act group must be 0 or 32");
     Ctx *c = find_ctx(set->device);
     if (!select_ctx(c)) return 0;
@@ -912,12 +968,12 @@ int coli_hip_moe_forward_dev(const ColiHipExpertSet *set, const float *x_dev, in
     const int tmax = (R + 31) / 32 + std::min(E, R);
     if (arm < 0) arm = forced_arm();
     if (arm < 0) arm = S == 1 ? COLI_HIP_ARM_GEMV : COLI_HIP_ARM_MFMA;
+    const MatGeom &gg = set->gg, &gd = set->gd;
 
     // table layout in one buffer
-    const size_t n_int = 4 + (size_t)E + (E + 1) + 3 * (size_t)R + (size_t)(S + 1) + R + 3 * (size_t)tmax;
-    const size_t tbl_b = n_int * 4 + (size_t)R * 4;
+    const size_t n_int = 4 + (size_t)E + (E + 1) + 3 * (size_t)R + 2 * (size_t)R + 3 * (size_t)tmax;
     Scratch s{};
-    if (!reserve_rows(c, set->gg, set->gd, S, R, ga, &s) || !reserve(c, c->tbl, tbl_b)) return 0;
+    if (!reserve_rows(c, gg, gd, S, R, ga, &s) || !reserve(c, c->tbl, n_int * 4)) return 0;
     int *p = (int *)c->tbl.p;
     TableOut t{};
     t.hdr = p;
@@ -932,9 +988,9 @@ int coli_hip_moe_forward_dev(const ColiHipExpertSet *set, const float *x_dev, in
     p += R;
     t.row_exp = p;
     p += R;
-    t.tok_ptr = p;
-    p += S + 1;
     t.tok_rows = p;
+    p += R;
+    t.tok_kk = p;
     p += R;
     t.mt_exp = p;
     p += tmax;
@@ -942,29 +998,73 @@ int coli_hip_moe_forward_dev(const ColiHipExpertSet *set, const float *x_dev, in
     p += tmax;
     t.mt_rend = p;
     p += tmax;
-    t.rw_row = (float *)p;
     c->tbl_view = t;
     c->tbl_E = E;
     c->tbl_R = R;
 
     Prof prof(c);
-    prof.mark(COLI_HIP_K_TABLE);
-    launch_build_table(ids_dev, w_dev, S, k, E, t, tmax, c->stream);
+    DispatchOpts opt;
+    opt.buf_ok = set->buf_ok;
+    const int act = epi_act(ga);
+    // one token routes to k distinct experts in top-k order, which is also
+    // batch-union order: row r is (token 0, slot r) and no table is needed
+    const bool one_token = S == 1 && arm == COLI_HIP_ARM_GEMV;
+    ExpertDesc *rdesc = nullptr;
+    if (one_token && logits_dev) {
+        if (!reserve(c, c->rdesc, (size_t)k * sizeof(ExpertDesc))) return 0;
+        rdesc = (ExpertDesc *)c->rdesc.p;
+    }
+    if (logits_dev) {
+        QuantArgs qa{x_dev, gg.K, S, gg.K, gg.Kp, s.xq, s.xs, s.sx, s.sxs, act};
+        prof.mark(COLI_HIP_K_QUANT_X);
+        launch_route_quant(logits_dev, S, E, k, ids_dev, w_dev, qa, set->desc_dev, rdesc, c->stream);
+        opt.x_quantized = true;
+    }
     RowPlan plan{};
-    plan.row_exp = t.row_exp;
-    plan.row_act = t.row_tok;
-    plan.mt_exp = t.mt_exp;
-    plan.mt_row0 = t.mt_row0;
-    plan.mt_rend = t.mt_rend;
-    plan.counts = t.hdr;
-    run_experts(c, prof, set->desc_dev, plan, set->gg, set->gd, x_dev, S, false, R, tmax, ga, arm, s);
+    if (one_token) {
+        c->tbl_view.hdr = nullptr;
+        plan.row_desc = rdesc;
+        plan.row_exp = ids_dev;
+        plan.row_act = ids_dev;   // unused (act_zero)
+        plan.counts = ids_dev;    // unused (n_rows_fixed)
+        opt.act_zero = true;
+        opt.n_rows_fixed = k;
+    } else {
+        prof.mark(COLI_HIP_K_TABLE);
+        launch_build_table(ids_dev, S, k, E, t, tmax, c->stream);
+        plan.row_exp = t.row_exp;
+        plan.row_act = t.row_tok;
+        plan.mt_exp = t.mt_exp;
+        plan.mt_row0 = t.mt_row0;
+        plan.mt_rend = t.mt_rend;
+        plan.counts = t.hdr;
+    }
+    run_experts(c, prof, set->desc_dev, plan, gg, gd, x_dev, S, false, R, tmax, ga, arm, s, opt);
     prof.mark(COLI_HIP_K_COMBINE);
-    launch_combine_padded(out_dev, s.y, t.tok_rows, t.rw_row, S, k, set->gd.O, s.ys, c->stream);
+    if (one_token)   // rows 0..k-1 of token 0, in top-k order
+        launch_combine_tok(out_dev, s.y, nullptr, nullptr, w_dev, 1, k, gd.O, s.ys, c->stream);
+    else
+        launch_combine_tok(out_dev, s.y, t.tok_rows, t.tok_kk, w_dev, S, k, gd.O, s.ys, c->stream);
     prof.mark(-1);
     if (!hip_ok(hipGetLastError(), "moe forward launch")) return 0;
     prof.finish();
     note_group(E, R);
     return 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+int coli_hip_moe_forward_dev(const ColiHipExpertSet *set, const float *x_dev, int S, const int *ids_dev,
+                             const float *w_dev, int k, float *out_dev, int ga, int arm) {
+    return moe_forward_impl(set, x_dev, S, nullptr, (int *)ids_dev, (float *)w_dev, k, out_dev, ga, arm);
+}
+
+int coli_hip_moe_forward_logits_dev(const ColiHipExpertSet *set, const float *x_dev, int S, const float *logits_dev,
+                                    int k, int *ids_dev, float *w_dev, float *out_dev, int ga, int arm) {
+    if (!logits_dev) return 0;
+    return moe_forward_impl(set, x_dev, S, logits_dev, ids_dev, w_dev, k, out_dev, ga, arm);
 }
 
 void *coli_hip_stream(int device) {
@@ -975,7 +1075,7 @@ void *coli_hip_stream(int device) {
 int coli_hip_last_table(int device, int *hdr, int *uexp, int *off, int *row_tok, int *tok_rows, int e_cap,
                         int r_cap) {
     Ctx *c = find_ctx(device);
-    if (!select_ctx(c) || !c->tbl_view.hdr) return 0;
+    if (!select_ctx(c) || !c->tbl_view.hdr) return fail("last_table: the last dispatch built no table");
     const TableOut &t = c->tbl_view;
     if (!hip_ok(hipStreamSynchronize(c->stream), "table sync")) return 0;
     const int E = std::min(c->tbl_E, e_cap), R = std::min(c->tbl_R, r_cap);

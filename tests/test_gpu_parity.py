@@ -241,6 +241,29 @@ def test_moe_layer_matches_oracle(hip, orc, ga, arm):
     assert np.array_equal(t["tok_rows"].reshape(S, k), o["tok_rows"])
 
 
+@pytest.mark.parametrize("S,arm", [(1, -1), (1, 0), (6, 2), (6, -1)])
+@pytest.mark.parametrize("ga", [32, 0])
+def test_moe_layer_fused_router_matches_oracle(hip, orc, S, arm, ga):
+    """Router fused with the x quantisation; one token on the GEMV arm runs
+    without an expert table, and the GEMV arm folds the combine into the down
+    projection."""
+    say("fused router layer", S, arm, ga)
+    rng = np.random.default_rng(300 + S + arm + ga)
+    E, D, I, k = 20, 320, 192, 6
+    gpu, ora, eset, x, logits = _layer_case(hip, orc, rng, E, D, I, S, k)
+    bx, bl = hip.DeviceBuffer.from_array(x), hip.DeviceBuffer.from_array(logits)
+    bids, bw, bout = hip.DeviceBuffer(S * k * 4), hip.DeviceBuffer(S * k * 4), hip.DeviceBuffer(S * D * 4)
+    for rep in range(3):   # repeats: the fused combine's counters reset themselves
+        hip.moe_forward_logits_dev(eset, bx.ptr, S, bl.ptr, k, bids.ptr, bw.ptr, bout.ptr, ga, arm)
+        hip.pipe_sync(0)
+        out = bout.download(np.float32, (S, D))
+        ids, w = orc.route_softmax_topk(logits, k)
+        assert np.array_equal(bids.download(np.int32, (S, k)), ids)
+        assert np.array_equal(bw.download(np.float32, (S, k)), w)
+        ref = orc.moe_forward(x, ids, w, ora, ga)
+        assert np.array_equal(out, ref), (rep, nerr(out, ref))
+
+
 def test_moe_layer_arms_agree_and_repeat(hip, orc):
     say("arms agree")
     rng = np.random.default_rng(77)
