@@ -38,12 +38,13 @@ __device__ __forceinline__ uint2 ldg_stream2(const void *p) {
     return make_uint2(v.x, v.y);
 }
 
-constexpr int TILE_O = 64;     // rows of a weight tile in the device layout
+constexpr int TILE_O = 32;     // rows of a weight tile in the device layout
 constexpr int BLK = 32;        // K elements per block (one MFMA K step)
 
 // One expert's three resident tensors as the kernels see them.
-// Weights are tiled [Op/64][nb][64][BB] (BB = 16 bytes int4, 32 bytes int8);
-// scales are tiled [Op/64][ng][64] f32.
+// Weights are tiled [Op/32][nb][32][BB] (BB = 16 bytes int4, 32 bytes int8);
+// scales are tiled [Op/32][ng][32] f32. One tile is the contiguous stream a
+// GEMV half-wave reads; Op is padded to 64 so tiles come in pairs.
 struct ExpertDesc {
     const uint8_t *w[3];   // gate, up, down
     const float *sc[3];
@@ -96,12 +97,16 @@ __device__ __forceinline__ long long trace_stamp() {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, 0x00020000);
 }
+// Weight streams are read once per pass: the loads carry the non-temporal
+// hint (cache-policy bit 1), which on gfx950 doubles the rate of a streaming
+// read against plain loads that allocate in the caches.
+constexpr int BUF_NT = 2;
 __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, BUF_NT);
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
 __device__ __forceinline__ float bloadf(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, BUF_NT));
 }
 
 // Index of the wavefront in its workgroup, known to the compiler as uniform.

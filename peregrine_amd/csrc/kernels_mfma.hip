@@ -87,9 +87,9 @@ __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const i
         int o = GATEUP ? n0 + j : n0 + s * 32 + j;
         oc[s] = o;
         if (o >= g.Op) o = g.Op - 1;
-        wp[s] = (const uint8_t *)gptr(a.desc[e].w[mat] + ((size_t)(o >> 6) * g.nb * TILE_O + (o & 63)) * BB +
+        wp[s] = (const uint8_t *)gptr(a.desc[e].w[mat] + ((size_t)(o / TILE_O) * g.nb * TILE_O + (o % TILE_O)) * BB +
                                       hh * (BB / 2));
-        sp[s] = (const float *)gptr(a.desc[e].sc[mat] + (size_t)(o >> 6) * g.ng * TILE_O + (o & 63));
+        sp[s] = (const float *)gptr(a.desc[e].sc[mat] + (size_t)(o / TILE_O) * g.ng * TILE_O + (o % TILE_O));
     }
 
     float acc[NSUB][16];

@@ -83,7 +83,7 @@ void launch_quant_rows(const QuantArgs &a, hipStream_t st) {
 //         the 16 bytes of each 32-block keep QT's nibble order.
 //   int8: each 8-element group is permuted to perm8 order so it lines up with
 //         the activation layout.
-// Scales become [Op/64][ng][64]; int4 scales are stored divided by 16 because
+// Scales become [Op/32][ng][32]; int4 scales are stored divided by 16 because
 // the unpacked int4 operands carry a factor 16 (exact: a power of two).
 // ---------------------------------------------------------------------------
 __global__ void repack_kernel(const uint8_t *raw, const float *raw_sc, int fmt, int I, int O, int gs, uint8_t *w,
@@ -92,7 +92,7 @@ __global__ void repack_kernel(const uint8_t *raw, const float *raw_sc, int fmt, 
     const size_t total = (size_t)g.Op * g.nb;
     if (idx >= total) return;
     const int o = (int)(idx / g.nb), b = (int)(idx % g.nb);
-    const int t = o >> 6, ol = o & 63;
+    const int t = o / TILE_O, ol = o % TILE_O;
     const bool grouped = (fmt == 4 || fmt == 8);
     if (g.w4) {
         const size_t rb = (size_t)(I + 1) / 2;

@@ -8,6 +8,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <vector>
 
@@ -16,12 +17,18 @@
 
 using namespace phip;
 
+namespace {
+struct Slab;
+}
+
 struct ColiHipTensor {
     int fmt, I, O, gs, device;
     MatGeom g;
-    uint8_t *w;
+    uint8_t *w;            // tiled weights; the scales follow in the same arena block
     float *sc;
     size_t w_bytes, sc_bytes;
+    Slab *slab;            // arena slab holding w and sc
+    size_t blk_off, blk_bytes;
 };
 
 struct ColiHipGraph {
@@ -85,6 +92,86 @@ int hip_ok(hipError_t e, const char *what) {
 int fail(const char *what) {
     std::fprintf(stderr, "[HIP] %s\n", what);
     return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Resident-tensor arena. Expert tensors are sub-allocated from large slabs
+// (512 MB, or one slab per larger tensor) instead of one small hipMalloc per
+// weight and scale buffer: a streaming kernel then reads a few large mappings
+// rather than hundreds of small ones, and a tensor's weights and scales sit in
+// one block. First fit over each slab's free ranges, coalesced on release; a
+// slab returns to the device when its last block is released.
+// ---------------------------------------------------------------------------
+size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
+
+struct Slab {
+    int device;
+    uint8_t *base;
+    size_t size, used;
+    std::map<size_t, size_t> free_ranges;   // offset -> length
+};
+
+constexpr size_t SLAB_BYTES = (size_t)512 << 20;
+constexpr size_t ARENA_ALIGN = 4096;
+std::mutex g_arena_mu;
+std::vector<Slab *> g_slabs;
+
+bool slab_take(Slab *s, size_t bytes, size_t *off) {
+    for (auto it = s->free_ranges.begin(); it != s->free_ranges.end(); ++it) {
+        if (it->second < bytes) continue;
+        *off = it->first;
+        const size_t rest = it->second - bytes;
+        s->free_ranges.erase(it);
+        if (rest) s->free_ranges[*off + bytes] = rest;
+        s->used += bytes;
+        return true;
+    }
+    return false;
+}
+
+// Caller has selected the device.
+Slab *arena_alloc(int device, size_t bytes, size_t *off) {
+    bytes = round_up(bytes, ARENA_ALIGN);
+    std::lock_guard<std::mutex> lock(g_arena_mu);
+    for (Slab *s : g_slabs)
+        if (s->device == device && slab_take(s, bytes, off)) return s;
+    Slab *s = new Slab{device, nullptr, std::max(SLAB_BYTES, round_up(bytes, (size_t)2 << 20)), 0, {}};
+    if (!hip_ok(hipMalloc(&s->base, s->size), "tensor arena slab")) {
+        delete s;
+        return nullptr;
+    }
+    s->free_ranges[0] = s->size;
+    g_slabs.push_back(s);
+    slab_take(s, bytes, off);
+    return s;
+}
+
+void arena_release(Slab *s, size_t off, size_t bytes) {
+    bytes = round_up(bytes, ARENA_ALIGN);
+    std::lock_guard<std::mutex> lock(g_arena_mu);
+    auto it = s->free_ranges.emplace(off, bytes).first;
+    if (it != s->free_ranges.begin()) {   // merge with the range before
+        auto prev = std::prev(it);
+        if (prev->first + prev->second == off) {
+            prev->second += it->second;
+            s->free_ranges.erase(it);
+            it = prev;
+        }
+    }
+    auto next = std::next(it);
+    if (next != s->free_ranges.end() && it->first + it->second == next->first) {
+        it->second += next->second;
+        s->free_ranges.erase(next);
+    }
+    s->used -= bytes;
+    if (s->used == 0) {
+        int cur = -1;
+        if (hipGetDevice(&cur) == hipSuccess && cur != s->device) (void)hipSetDevice(s->device);
+        hipFree(s->base);
+        if (cur >= 0 && cur != s->device) (void)hipSetDevice(cur);
+        g_slabs.erase(std::find(g_slabs.begin(), g_slabs.end(), s));
+        delete s;
+    }
 }
 
 int env_int(const char *name, int dflt) {
@@ -177,7 +264,6 @@ void free_ctx(Ctx *c) {
     c->stream = nullptr;
 }
 
-size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 
 int make_geom(int fmt, int I, int O, int gs, MatGeom *g) {
     const bool grouped = fmt == COLI_HIP_FMT_I4G || fmt == COLI_HIP_FMT_I8G;
@@ -212,8 +298,7 @@ size_t raw_scale_count(const MatGeom &g) { return (size_t)g.O * g.ng; }
 
 void tensor_release(ColiHipTensor *t) {
     if (!t) return;
-    if (t->w) hipFree(t->w);
-    if (t->sc) hipFree(t->sc);
+    if (t->slab) arena_release(t->slab, t->blk_off, t->blk_bytes);
     std::free(t);
 }
 
@@ -257,11 +342,14 @@ int upload_impl(ColiHipTensor **tensor, const void *weights, const float *scales
     t->g = g;
     t->w_bytes = (size_t)g.Op * g.nb * (g.w4 ? 16 : 32);
     t->sc_bytes = (size_t)g.Op * g.ng * sizeof(float);
-    if (!hip_ok(hipMalloc(&t->w, t->w_bytes), "tensor allocation") ||
-        !hip_ok(hipMalloc(&t->sc, t->sc_bytes), "scale allocation")) {
+    t->blk_bytes = round_up(t->w_bytes, 256) + t->sc_bytes;
+    t->slab = arena_alloc(device, t->blk_bytes, &t->blk_off);
+    if (!t->slab) {
         tensor_release(t);
         return 0;
     }
+    t->w = t->slab->base + t->blk_off;
+    t->sc = (float *)(t->w + round_up(t->w_bytes, 256));
     const int ok = from_device ? repack_into(c, t, weights, scales) : repack_from_host(c, t, weights, scales);
     if (!ok) {
         tensor_release(t);
