@@ -194,61 +194,85 @@ void launch_combine_tok(float *out, const float *y, const int *tok_rows, const i
 // then w_j = exp(l_j - l_0) / sum_j exp(l_j - l_0) summed in selection order.
 // One wavefront per token.
 // ---------------------------------------------------------------------------
-// One wavefront routes one token. Top-k by rank: element e's rank is the
-// number of valid logits that beat it (greater, or equal with a lower index);
-// NaN and -inf never qualify, exactly as the strict `>` scan of the greedy loop
-// (router.rs:97-118) never picks them. The k lowest ranks are the greedy
-// selection in order. lv: LDS scratch of E floats (E <= 1024); selv/seli: 16.
-// desc/row_desc (optional): copy the chosen experts' descriptors per slot.
+// (value desc, index asc) maximum across the wavefront, returned uniform.
+// DPP exchanges inside each row of 16 lanes (quad swaps, half-row and row
+// mirrors leave all 16 lanes agreeing), then the four row results are read
+// as scalars.
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp(float &v, int &i) {
+    const float ov = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+    const int oi = __builtin_amdgcn_update_dpp(0, i, CTRL, 0xF, 0xF, false);
+    if (ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
+    }
+}
+__device__ __forceinline__ void wave_argmax(float &v, int &i) {
+    argmax_dpp<0xB1>(v, i);    // quad_perm [1,0,3,2]
+    argmax_dpp<0x4E>(v, i);    // quad_perm [2,3,0,1]
+    argmax_dpp<0x141>(v, i);   // row_half_mirror
+    argmax_dpp<0x140>(v, i);   // row_mirror
+    float bv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    int bi = __builtin_amdgcn_readlane(i, 0);
+#pragma unroll
+    for (int r = 16; r < 64; r += 16) {
+        const float rv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), r));
+        const int ri = __builtin_amdgcn_readlane(i, r);
+        if (rv > bv || (rv == bv && ri < bi)) {
+            bv = rv;
+            bi = ri;
+        }
+    }
+    v = bv;
+    i = bi;
+}
+
+// One wavefront routes one token with the greedy loop itself: k rounds, each
+// picking the largest remaining logit, ties to the lowest index. A lane holds
+// logits e = lane + 64*j; it reduces them in ascending j with a strict `>`,
+// then the wave reduces (value desc, index asc) across lanes. NaN and -inf
+// never qualify (a strict `>` against -inf never picks them), so fewer than k
+// valid logits leave the remaining slots empty, exactly as router.rs:97-118.
+// The winner's owner retires it. desc/row_desc (optional): copy the chosen
+// experts' descriptors per slot.
 template <int PER>
-__device__ void route_token(const float *l, int E, int k, int *ids, float *w, float *lv, float *selv, int *seli,
-                            const ExpertDesc *desc, ExpertDesc *row_desc) {
+__device__ void route_token(const float *l, int E, int k, int *ids, float *w, const ExpertDesc *desc,
+                            ExpertDesc *row_desc) {
     const int lane = threadIdx.x & 63;
-    for (int e = lane; e < E; e += 64) lv[e] = l[e];
-    __builtin_amdgcn_wave_barrier();   // one wavefront: LDS ops complete in order
     float ve[PER];
-    int rank[PER];
-    bool valid[PER];
-    int nvalid = 0;
 #pragma unroll
     for (int j = 0; j < PER; j++) {
         const int e = lane + 64 * j;
-        ve[j] = e < E ? lv[e] : -INFINITY;
-        valid[j] = ve[j] > -INFINITY;   // false for NaN, -inf and padding
-        nvalid += valid[j];
-        rank[j] = 0;
+        const float v = e < E ? l[e] : -INFINITY;
+        ve[j] = v > -INFINITY ? v : -INFINITY;   // NaN, -inf and padding never qualify
     }
-    // every lane streams all E logits (broadcast LDS reads, 16 at a time)
-    for (int e0 = 0; e0 < E; e0 += 16) {
-        float v2[16];
+    float myv = -INFINITY;   // lane kk keeps the kk-th pick
+    int myid = 0, kept = 0;
+    for (int kk = 0; kk < k; kk++) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
 #pragma unroll
-        for (int q = 0; q < 16; q++) v2[q] = e0 + q < E ? lv[e0 + q] : -INFINITY;
-#pragma unroll
-        for (int q = 0; q < 16; q++) {
-            const int e2 = e0 + q;
-#pragma unroll
-            for (int j = 0; j < PER; j++) {
-                const int e = lane + 64 * j;
-                rank[j] += (v2[q] > ve[j]) | ((v2[q] == ve[j]) & (e2 < e));
+        for (int j = 0; j < PER; j++)
+            if (ve[j] > bv) {
+                bv = ve[j];
+                bi = lane + 64 * j;
             }
+        wave_argmax(bv, bi);
+        if (!(bv > -INFINITY)) break;   // uniform: nothing valid remains
+        if (lane == kk) {
+            myv = bv;
+            myid = bi;
         }
+        if ((bi & 63) == lane) ve[bi >> 6] = -INFINITY;   // retire the pick (PER is small: unrolled select)
+        kept++;
     }
-#pragma unroll
-    for (int j = 0; j < PER; j++) {
-        if (valid[j] && rank[j] < k) {
-            selv[rank[j]] = ve[j];
-            seli[rank[j]] = lane + 64 * j;
-        }
-    }
-    for (int off = 32; off > 0; off >>= 1) nvalid += __shfl_xor(nvalid, off);
-    __builtin_amdgcn_wave_barrier();
-    const int kept = nvalid < k ? nvalid : k;
-    const float myex = lane < kept ? exp_cr(__fsub_rn(selv[lane], selv[0])) : 0.0f;
+    const float l0 = __shfl(myv, 0);
+    const float myex = lane < kept ? exp_cr(__fsub_rn(myv, l0)) : 0.0f;
     float z = 0.0f;
     for (int kk = 0; kk < kept; kk++) z = __fadd_rn(z, __shfl(myex, kk));
     if (lane < k) {
         const bool ok = lane < kept;
-        const int id = ok ? seli[lane] : 0;
+        const int id = ok ? myid : 0;
         ids[lane] = id;
         w[lane] = ok ? __fdiv_rn(myex, z) : 0.0f;
         if (row_desc) row_desc[lane] = desc[id];
@@ -257,11 +281,8 @@ __device__ void route_token(const float *l, int E, int k, int *ids, float *w, fl
 
 template <int PER>
 __global__ __launch_bounds__(64) void route_softmax_kernel(const float *logits, int E, int k, int *ids, float *w) {
-    __shared__ float lv[1024], selv[16];
-    __shared__ int seli[16];
     const int s = blockIdx.x;
-    route_token<PER>(logits + (size_t)s * E, E, k, ids + (size_t)s * k, w + (size_t)s * k, lv, selv, seli, nullptr,
-                     nullptr);
+    route_token<PER>(logits + (size_t)s * E, E, k, ids + (size_t)s * k, w + (size_t)s * k, nullptr, nullptr);
 }
 
 // Router fused with the activation quantisation of the same token. Grid
@@ -273,11 +294,10 @@ template <int PER>
 __global__ __launch_bounds__(256) void route_quant_kernel(const float *logits, int E, int k, int *ids, float *w,
                                                           QuantArgs a, const ExpertDesc *desc,
                                                           ExpertDesc *row_desc) {
-    __shared__ float lv[1024], selv[16], red[4];
-    __shared__ int seli[16];
+    __shared__ float red[4];
     const int s = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     if (blockIdx.y == 0 && wave == 0)
-        route_token<PER>(logits + (size_t)s * E, E, k, ids + (size_t)s * k, w + (size_t)s * k, lv, selv, seli, desc,
+        route_token<PER>(logits + (size_t)s * E, E, k, ids + (size_t)s * k, w + (size_t)s * k, desc,
                          row_desc ? row_desc + (size_t)s * k : nullptr);
     const float *x = a.x + (size_t)s * a.x_stride;
     int8_t *q = a.q + (size_t)s * a.q_stride;
