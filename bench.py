@@ -55,6 +55,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--experts", type=int, default=None, help="override the resident expert count (experiments)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 256 MiB device-to-device copy kernel 5 times (scales rocprofv3 "
+                         "FETCH_SIZE/WRITE_SIZE to bytes)")
     return ap.parse_args()
 
 
@@ -146,8 +149,48 @@ def cpu_baseline(cfg, wfmt, ga, seconds):
                        f"{wfmt} gs=32, act group {ga}), AVX2 int4 dot, {threads} threads over experts")
 
 
+METRIC = "MoE-layer tokens/s + HBM GB/s % peak (decode) / int8 MFMA % peak (prefill)"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_pmc.md")
+
+
+def calibrate_copy():
+    """A copy kernel of known size for scaling the PMC byte counters."""
+    import torch
+    n = 256 << 20
+    a = torch.ones(n, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes_read": n, "bytes_written": n, "launches": 5}))
+
+
+def measured_traffic(workload, kernel_prefix):
+    """HBM bytes per launch of the dominant (gate/up) kernel, from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE per dispatch, scaled by
+    the copy-kernel calibration); None when that workload was not profiled."""
+    try:
+        lines = open(TRAFFIC_FILE).read().splitlines()
+    except OSError:
+        return None
+    for ln in lines:
+        cells = [c.strip() for c in ln.strip().strip("|").split("|")]
+        if len(cells) < 3 or cells[0] != workload or kernel_prefix + "<" not in cells[1]:
+            continue
+        targs = [t.strip() for t in cells[1].split("<", 1)[1].rstrip(">").split(",")]
+        if len(targs) >= 3 and targs[2] == "true":   # the gate/up instantiation
+            try:
+                return int(float(cells[-1]))
+            except ValueError:
+                return None
+    return None
+
+
 def main():
     args = parse()
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1 "
                                    "(no collectives or sharding in scope)"}))
@@ -239,14 +282,14 @@ def main():
     if prefill:
         achieved = gu_ops / (gu_ms * 1e-3) / 1e12
         roof = dict(bound="mfma", achieved=round(achieved, 2), peak=INT8_PEAK_TOPS, unit="TFLOP/s",
-                    frac=round(achieved / INT8_PEAK_TOPS, 4), traffic=None)
+                    frac=round(achieved / INT8_PEAK_TOPS, 4), traffic=measured_traffic(cfg["name"], "mfma_kernel"))
     else:
         achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
         roof = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None)
+                    frac=round(achieved / HBM_PEAK_GBS, 4), traffic=measured_traffic(cfg["name"], "gemv_kernel"))
     value = S * L * steps / wall
     line = {
-        "metric": "MoE-layer tokens/s",
+        "metric": METRIC,
         "value": round(value, 2),
         "unit": "tokens/s",
         "n_gpus": 1,

@@ -164,8 +164,9 @@ void coli_hip_reset_stats(void);
 int coli_hip_set_debug_dots(int32_t *gateup_dev, int32_t *down_dev);
 /* Tuning hook: when set (device pointers, may be NULL), GEMV-arm workgroups
  * write 8 int64 per workgroup (index y*grid_x + x): phase timestamps of the
- * 100 MHz constant clock (entry, first weights in, blocks done, barrier,
- * chain done, exit) and the hardware CU id. */
+ * 100 MHz constant clock (entry, activations staged, first round ready, last
+ * round ready, chain done, exit) and the hardware CU id. Library built with
+ * -DPHIP_GEMV_TRACE only; otherwise ignored. */
 int coli_hip_set_debug_trace(long long *gateup_dev, long long *down_dev);
 /* Last row plan of the device-resident path, copied to host (for tests):
  * hdr[4] = {rows, tiles, distinct experts, 0}. */

@@ -419,7 +419,7 @@ struct Prof {
     explicit Prof(Ctx *ctx) : c(ctx), on(profiling() != 0) {
         if (!on) return;
         for (auto &e : c->ev)
-            if (!e && hipEventCreate(&e) != hipSuccess) on = false;
+            if (!e && hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) on = false;
     }
     void mark(int w) {   // event before kernel w (w = -1: final)
         if (!on || n >= N_EVENTS) return;

@@ -365,3 +365,27 @@ def test_greedy_argmax_token_identical(hip, orc):
                 tok_o = nxt
                 seq_o.append(nxt)
     assert np.array_equal(np.array(seq_g), np.array(seq_o))
+
+
+@pytest.mark.parametrize("arm", [-1, 0, 2])
+def test_golden_layer_bit_exact(hip, arm):
+    """The committed fixture (tests/golden/moe_layer_small.npz): device
+    routing, table, both activation-scale modes and every arm reproduce the
+    stored oracle outputs bit-for-bit."""
+    import os
+    say("golden layer", arm)
+    f = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "moe_layer_small.npz"))
+    E, D, I, S, k = (int(v) for v in f["dims"])
+    gpu = [hip.GpuExpert.upload_grouped(0, (f[f"e{e}_gate_q"], f[f"e{e}_gate_s"]),
+                                        (f[f"e{e}_up_q"], f[f"e{e}_up_s"]),
+                                        (f[f"e{e}_down_q"], f[f"e{e}_down_s"]), D, I, qt.FMT_I4G, 32)
+           for e in range(E)]
+    eset = hip.ExpertSet(gpu)
+    bx, bl = hip.DeviceBuffer.from_array(f["x"]), hip.DeviceBuffer.from_array(f["logits"])
+    bids, bw, bout = hip.DeviceBuffer(S * k * 4), hip.DeviceBuffer(S * k * 4), hip.DeviceBuffer(S * D * 4)
+    for ga in (0, 32):
+        hip.moe_forward_logits_dev(eset, bx.ptr, S, bl.ptr, k, bids.ptr, bw.ptr, bout.ptr, ga, arm)
+        hip.pipe_sync(0)
+        assert np.array_equal(bids.download(np.int32, (S, k)), f["ids"])
+        assert bw.download(np.float32, (S, k)).tobytes() == f["w"].tobytes()
+        assert bout.download(np.float32, (S, D)).tobytes() == f[f"y_ga{ga}"].tobytes(), ga
