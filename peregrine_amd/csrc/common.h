@@ -109,6 +109,11 @@ __device__ __forceinline__ float bloadf(__amdgpu_buffer_rsrc_t r, int voff, int 
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, BUF_NT));
 }
 
+// Read-only views in the constant address space: uniform loads through them
+// become scalar loads (reads only).
+typedef const __attribute__((address_space(4))) int CInt;
+typedef const __attribute__((address_space(4))) float CFloat;
+
 // Index of the wavefront in its workgroup, known to the compiler as uniform.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
