@@ -40,6 +40,7 @@ __device__ __forceinline__ uint2 ldg_stream2(const void *p) {
 
 constexpr int TILE_O = 32;     // rows of a weight tile in the device layout
 constexpr int BLK = 32;        // K elements per block (one MFMA K step)
+constexpr int MT_ROWS = 32;    // rows of one M tile of the grouped GEMM
 
 // One expert's three resident tensors as the kernels see them.
 // Weights are tiled [Op/32][nb][32][BB] (BB = 16 bytes int4, 32 bytes int8);

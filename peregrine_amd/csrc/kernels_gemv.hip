@@ -70,14 +70,13 @@ __device__ __forceinline__ void spin_until_geq(int *ctr, int target) {
 // blocks; in round c streaming wave w owns blocks c*NW*CH + w*CH + [0, CH).
 // A streaming wave issues its CH weight (and scale) loads for a round as one
 // batch — unconditional, clamped to the last block, so the wait counts stay
-// exact — (PF = 1: the next round's batch is issued before this one is used),
-// turns each block into its integer dot and its f32 factor (sw*sx[b] for
+// exact — turns each block into its integer dot and its f32 factor (sw*sx[b] for
 // 32-block activation scales, sw for grouped weights) and parks them in an
 // LDS ring of RING rounds. The chain wave walks each finished round in block
 // order while later rounds stream; a streaming wave waits only when it is
 // RING rounds ahead of the chain. Per-row weight scales only sum integers.
 // All waits are bounded.
-template <bool W4, int EPI, bool GATEUP, int NW, int CH, int PF>
+template <bool W4, int EPI, bool GATEUP, int NW, int CH>
 __global__ __launch_bounds__((NW + 1) * 64) void gemv_kernel(DotArgs a, MatGeom g, const int8_t *__restrict__ xq,
                                                              const float *__restrict__ sxv) {
     constexpr int BB = W4 ? 16 : 32;
@@ -125,8 +124,8 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemv_kernel(DotArgs a, MatGeom 
 
     const int nb = g.nb;
     const int nrounds = (nb + RB - 1) / RB;
-    WBlk<W4> wA[CH], wB[CH];
-    float sA[CH], sB[CH];
+    WBlk<W4> wA[CH];
+    float sA[CH];
     int xr[CH][8];       // this wave's activation blocks for the round (uniform: SGPRs)
     float sxr[CH];
     auto load_round = [&](int c, WBlk<W4> (&wv)[CH], float (&sv)[CH]) {
@@ -221,24 +220,10 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemv_kernel(DotArgs a, MatGeom 
     int gsum = 0;        // EPI_GRP: open group's integer sum
     int isum = 0;        // EPI_ROW: exact integer sum
     if (!chainer) {
-        if constexpr (PF) {
-            // two register sets alternate; the next round's loads are in
-            // flight while this round is turned into ring entries
 #pragma unroll 1
-            for (int c = 0; c < nrounds; c += 2) {
-                load_round(min(c + 1, nrounds - 1), wB, sB);
-                compute_round(c, wA, sA);
-                if (c + 1 < nrounds) {
-                    load_round(min(c + 2, nrounds - 1), wA, sA);
-                    compute_round(c + 1, wB, sB);
-                }
-            }
-        } else {
-#pragma unroll 1
-            for (int c = 0; c < nrounds; ++c) {
-                if (c > 0) load_round(c, wA, sA);
-                compute_round(c, wA, sA);
-            }
+        for (int c = 0; c < nrounds; ++c) {
+            if (c > 0) load_round(c, wA, sA);
+            compute_round(c, wA, sA);
         }
     } else {
 #ifdef EXP_NOSYNC
@@ -338,22 +323,25 @@ void set_lds_limit(int bytes) { g_lds_limit = bytes > 0 ? bytes : 64 * 1024; }
 
 // gate/up: 7 streaming waves + 1 chain wave (512 threads); down: 3 + 1.
 // Batches of 8 int4 blocks (4 int8 blocks): 4 KB of weights per wave in flight.
-template <bool W4, int EPI, bool GATEUP>
-static void launch_gemv_t(const DotArgs &a, const MatGeom &g, int grid_rows, hipStream_t st) {
-    constexpr int NW = GATEUP ? 7 : 3, CH = W4 ? 8 : 4;
+template <bool W4, int EPI, bool GATEUP, int CH>
+static void launch_gemv_c(const DotArgs &a, const MatGeom &g, int grid_rows, hipStream_t st) {
+    constexpr int NW = GATEUP ? 7 : 3;
     const size_t per_block = 64 * (4 + (W4 ? 2 : 4));
     const size_t lds = (size_t)GEMV_RING * NW * CH * per_block;
-    static const int pf = [] {
-        const char *v = std::getenv("COLI_HIP_GEMV_PF");
-        return v && *v ? std::atoi(v) : 0;
-    }();
-    auto kern = pf ? gemv_kernel<W4, EPI, GATEUP, NW, CH, 1> : gemv_kernel<W4, EPI, GATEUP, NW, CH, 0>;
-    static size_t attr_set[2] = {64 * 1024, 64 * 1024};   // dynamic LDS above 64 KB needs an explicit opt-in
-    if (lds > attr_set[pf ? 1 : 0] &&
+    auto kern = gemv_kernel<W4, EPI, GATEUP, NW, CH>;
+    static size_t attr_set = 64 * 1024;   // dynamic LDS above 64 KB needs an explicit opt-in
+    if (lds > attr_set &&
         hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess)
-        attr_set[pf ? 1 : 0] = lds;
+        attr_set = lds;
     dim3 grid(GATEUP ? (unsigned)((g.O + 31) / 32) : (unsigned)((g.O + 63) / 64), (unsigned)grid_rows);
     hipLaunchKernelGGL(kern, grid, dim3((NW + 1) * 64), lds, st, a, g, a.xq, a.sx);
+}
+
+// gate/up: 7 streaming waves + 1 chain wave (512 threads); down: 3 + 1.
+// Batches of 8 int4 blocks (4 int8 blocks): 4 KB of weights per wave per round.
+template <bool W4, int EPI, bool GATEUP>
+static void launch_gemv_t(const DotArgs &a, const MatGeom &g, int grid_rows, hipStream_t st) {
+    launch_gemv_c<W4, EPI, GATEUP, W4 ? 8 : 4>(a, g, grid_rows, st);
 }
 
 template <bool GATEUP>

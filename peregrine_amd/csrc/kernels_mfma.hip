@@ -101,19 +101,21 @@ __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const i
         iacc[s] = v16i{};
     }
 
-    // software pipeline: operands of block b+1 load while block b computes
-    v4i A = *(const v4i *)xa;
-    v4i B[NSUB];
+    // Software pipeline, two blocks ahead: three operand slots rotate through
+    // a loop unrolled by three. Loads are unconditional (clamped to the last
+    // block) so the wait counts stay exact; the weight scales travel with
+    // their block instead of being fetched when the epilogue needs them.
+    const int nrow = rend - r0;   // rows of this tile (1..32)
+    auto load_blk = [&](int b, v4i &A, v4i (&B)[NSUB], float (&S)[NSUB]) {
+        const int bc = b < g.nb ? b : g.nb - 1;
+        A = *(const v4i *)(xa + (size_t)bc * BLK);
 #pragma unroll
-    for (int s = 0; s < NSUB; ++s) B[s] = load_b<W4>(wp[s]);
-
-    for (int b = 0; b < g.nb; ++b) {
-        v4i An = A, Bn[NSUB];
-        const int bn = b + 1 < g.nb ? b + 1 : b;
-        An = *(const v4i *)(xa + (size_t)bn * BLK);
-#pragma unroll
-        for (int s = 0; s < NSUB; ++s) Bn[s] = load_b<W4>(wp[s] + (size_t)bn * TILE_O * BB);
-
+        for (int s = 0; s < NSUB; ++s) {
+            B[s] = load_b<W4>(wp[s] + (size_t)bc * TILE_O * BB);
+            if constexpr (EPI != EPI_ROW) S[s] = sp[s][(size_t)grp_of(bc, g.gshift) * TILE_O];
+        }
+    };
+    auto do_blk = [&](int b, const v4i &A, const v4i (&B)[NSUB], const float (&S)[NSUB]) {
         const bool gend = grp_end(b, g.gshift, g.nb);
 #pragma unroll
         for (int s = 0; s < NSUB; ++s) {
@@ -133,31 +135,48 @@ __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const i
                 iacc[s] = d;
             } else if constexpr (EPI == EPI_GRP) {
                 if (gend) {
-                    const float sw = sp[s][(size_t)grp_of(b, g.gshift) * TILE_O];
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) acc[s][i] = __fadd_rn(acc[s][i], __fmul_rn((float)d[i], sw));
+                    for (int gq = 0; gq < 4; ++gq) {
+                        if (8 * gq >= nrow) break;   // uniform: rows past the tile's end
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+                            const int i = 4 * gq + t;
+                            acc[s][i] = __fadd_rn(acc[s][i], __fmul_rn((float)d[i], S[s]));
+                        }
+                    }
                     iacc[s] = v16i{};
                 } else {
                     iacc[s] = d;
                 }
             } else {
-                const float sw = sp[s][(size_t)grp_of(b, g.gshift) * TILE_O];
                 const float4 *sx4 = (const float4 *)(sxl + b * 32 + 4 * hh);
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const float4 sq = sx4[2 * q];
+                for (int gq = 0; gq < 4; ++gq) {
+                    if (8 * gq >= nrow) break;   // uniform: rows past the tile's end
+                    const float4 sq = sx4[2 * gq];
+                    const float sxr[4] = {sq.x, sq.y, sq.z, sq.w};
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
-                        const float sxr = t == 0 ? sq.x : t == 1 ? sq.y : t == 2 ? sq.z : sq.w;
-                        const int i = 4 * q + t;
-                        acc[s][i] = __fmaf_rn(__fmul_rn(sw, sxr), (float)d[i], acc[s][i]);
+                        const int i = 4 * gq + t;
+                        acc[s][i] = __fmaf_rn(__fmul_rn(S[s], sxr[t]), (float)d[i], acc[s][i]);
                     }
                 }
             }
         }
-        A = An;
-#pragma unroll
-        for (int s = 0; s < NSUB; ++s) B[s] = Bn[s];
+    };
+    v4i A0, A1, A2;
+    v4i B0[NSUB], B1[NSUB], B2[NSUB];
+    float S0[NSUB], S1[NSUB], S2[NSUB];
+    load_blk(0, A0, B0, S0);
+    load_blk(1, A1, B1, S1);
+#pragma unroll 1
+    for (int b = 0; b < g.nb; b += 3) {
+        load_blk(b + 2, A2, B2, S2);
+        do_blk(b, A0, B0, S0);
+        load_blk(b + 3, A0, B0, S0);
+        if (b + 1 < g.nb) do_blk(b + 1, A1, B1, S1);
+        load_blk(b + 4, A1, B1, S1);
+        if (b + 2 < g.nb) do_blk(b + 2, A2, B2, S2);
     }
 
     // per-row activation scale (EPI_ROW / EPI_GRP) of each accumulator row

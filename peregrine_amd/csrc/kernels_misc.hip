@@ -465,21 +465,21 @@ __global__ __launch_bounds__(1024) void build_table_kernel(const int *ids, int S
         const int u = u0 + tid;
         const int c = u < n_u ? cnt[uex[u]] : 0;
         const int off = block_exclusive_scan(c, scan_tmp) + (u0 ? s_carry[0] : 0);
-        const int mt = block_exclusive_scan((c + 31) / 32, scan_tmp) + (u0 ? s_carry[1] : 0);
+        const int mt = block_exclusive_scan((c + MT_ROWS - 1) / MT_ROWS, scan_tmp) + (u0 ? s_carry[1] : 0);
         if (u < n_u) {
             const int e = uex[u];
             fill[e] = off;
             t.uexp[u] = e;
             t.off[u] = off;
-            for (int j = 0; j < (c + 31) / 32 && mt + j < tmax; j++) {
+            for (int j = 0; j < (c + MT_ROWS - 1) / MT_ROWS && mt + j < tmax; j++) {
                 t.mt_exp[mt + j] = e;
-                t.mt_row0[mt + j] = off + 32 * j;
+                t.mt_row0[mt + j] = off + MT_ROWS * j;
                 t.mt_rend[mt + j] = off + c;
             }
             if (u == n_u - 1) {
                 t.off[n_u] = off + c;
                 t.hdr[0] = off + c;
-                t.hdr[1] = mt + (c + 31) / 32;
+                t.hdr[1] = mt + (c + MT_ROWS - 1) / MT_ROWS;
                 t.hdr[2] = n_u;
                 t.hdr[3] = 0;
             }
@@ -487,7 +487,7 @@ __global__ __launch_bounds__(1024) void build_table_kernel(const int *ids, int S
         __syncthreads();
         if (tid == nth - 1) {
             s_carry[0] = off + c;
-            s_carry[1] = mt + (c + 31) / 32;
+            s_carry[1] = mt + (c + MT_ROWS - 1) / MT_ROWS;
         }
         __syncthreads();
     }

@@ -579,7 +579,7 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
 
     // host-built plan: descriptors in call order, rows consecutive
     int T = 0;
-    for (int i = 0; i < count; i++) T += (rows[i] + 31) / 32;
+    for (int i = 0; i < count; i++) T += (rows[i] + MT_ROWS - 1) / MT_ROWS;
     const int s_n = red ? red->s_n : 0;
     const size_t n_int = (size_t)total /*row_exp*/ + 3 * (size_t)T + 2 + (red ? (size_t)(s_n + 1) + total : 0);
     const size_t desc_b = round_up((size_t)count * sizeof(ExpertDesc), 16);
@@ -609,7 +609,7 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
     float *rwv = (float *)(ri + (red ? total : 0));
     for (int i = 0, r = 0, t = 0; i < count; i++) {
         for (int q = 0; q < rows[i]; q++) row_exp[r + q] = i;
-        for (int q = 0; q < rows[i]; q += 32, t++) {
+        for (int q = 0; q < rows[i]; q += MT_ROWS, t++) {
             mt_exp[t] = i;
             mt_row0[t] = r + q;
             mt_rend[t] = r + rows[i];
@@ -1053,7 +1053,7 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
     Ctx *c = find_ctx(set->device);
     if (!select_ctx(c)) return 0;
     const int E = set->count, R = S * k;
-    const int tmax = (R + 31) / 32 + std::min(E, R);
+    const int tmax = (R + MT_ROWS - 1) / MT_ROWS + std::min(E, R);
     if (arm < 0) arm = forced_arm();
     if (arm < 0) arm = S == 1 ? COLI_HIP_ARM_GEMV : COLI_HIP_ARM_MFMA;
     const MatGeom &gg = set->gg, &gd = set->gd;
