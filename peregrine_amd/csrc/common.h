@@ -38,6 +38,19 @@ __device__ __forceinline__ uint2 ldg_stream2(const void *p) {
     return make_uint2(v.x, v.y);
 }
 
+// The same through global-address-space pointers: global (not flat) loads,
+// which count only against vmcnt, so LDS waits never wait on them.
+typedef const __attribute__((address_space(1))) uint8_t GU8;
+typedef const __attribute__((address_space(1))) float GF32;
+__device__ __forceinline__ uint4 ldg_stream4g(GU8 *p) {
+    const u32x4 v = __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4 *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ldg_stream2g(GU8 *p) {
+    const u32x2 v = __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x2 *)p);
+    return make_uint2(v.x, v.y);
+}
+
 constexpr int TILE_O = 32;     // rows of a weight tile in the device layout
 constexpr int BLK = 32;        // K elements per block (one MFMA K step)
 constexpr int MT_ROWS = 32;    // rows of one M tile of the grouped GEMM

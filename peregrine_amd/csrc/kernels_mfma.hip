@@ -25,16 +25,16 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 template <bool W4>
-__device__ __forceinline__ v4i load_b(const uint8_t *p) {
+__device__ __forceinline__ v4i load_b(GU8 *p) {
     v4i r;
     if constexpr (W4) {
-        const uint2 w = ldg_stream2(p);
+        const uint2 w = ldg_stream2g(p);
         r[0] = i4_even16(w.x);
         r[1] = i4_odd16(w.x);
         r[2] = i4_even16(w.y);
         r[3] = i4_odd16(w.y);
     } else {
-        const uint4 w = ldg_stream4(p);
+        const uint4 w = ldg_stream4g(p);
         r[0] = (int)w.x;
         r[1] = (int)w.y;
         r[2] = (int)w.z;
@@ -47,7 +47,7 @@ __device__ __forceinline__ int acc_row(int reg, int lane) { return 8 * (reg >> 2
 
 // NSUB column subtiles of 32 per wave. GATEUP: subtile 0 = gate, 1 = up (same
 // channels). Down: NSUB adjacent 32-channel subtiles.
-template <bool W4, int EPI, bool GATEUP, int NSUB>
+template <bool W4, int EPI, bool GATEUP, int NSUB, int PD>
 __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const int8_t *__restrict__ xq,
                                                    const float *__restrict__ sxv) {
     constexpr int BB = W4 ? 16 : 32;
@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const i
     int ra = r0 + j;
     if (ra >= rend) ra = rend - 1;
     const int arow_a = a.act_identity ? ra : a.plan.row_act[ra];
-    const int8_t *xa = xq + (size_t)arow_a * a.x_stride + hh * 16;
+    GU8 *xa = (GU8 *)gptr(xq + (size_t)arow_a * a.x_stride + hh * 16);
 
     if constexpr (EPI == EPI_B32) {
         for (int idx = threadIdx.x; idx < 32 * g.nb; idx += 256) {
@@ -78,8 +78,8 @@ __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const i
         __syncthreads();
     }
 
-    const uint8_t *wp[NSUB];
-    const float *sp[NSUB];
+    GU8 *wp[NSUB];
+    GF32 *sp[NSUB];
     int oc[NSUB];
 #pragma unroll
     for (int s = 0; s < NSUB; ++s) {
@@ -87,9 +87,8 @@ __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const i
         int o = GATEUP ? n0 + j : n0 + s * 32 + j;
         oc[s] = o;
         if (o >= g.Op) o = g.Op - 1;
-        wp[s] = (const uint8_t *)gptr(a.desc[e].w[mat] + ((size_t)(o / TILE_O) * g.nb * TILE_O + (o % TILE_O)) * BB +
-                                      hh * (BB / 2));
-        sp[s] = (const float *)gptr(a.desc[e].sc[mat] + (size_t)(o / TILE_O) * g.ng * TILE_O + (o % TILE_O));
+        wp[s] = gptr(a.desc[e].w[mat] + ((size_t)(o / TILE_O) * g.nb * TILE_O + (o % TILE_O)) * BB + hh * (BB / 2));
+        sp[s] = gptr(a.desc[e].sc[mat] + (size_t)(o / TILE_O) * g.ng * TILE_O + (o % TILE_O));
     }
 
     float acc[NSUB][16];
@@ -101,14 +100,14 @@ __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const i
         iacc[s] = v16i{};
     }
 
-    // Software pipeline, two blocks ahead: three operand slots rotate through
-    // a loop unrolled by three. Loads are unconditional (clamped to the last
+    // Software pipeline, PD blocks ahead: PD + 1 operand slots rotate through
+    // a loop unrolled by PD + 1. Loads are unconditional (clamped to the last
     // block) so the wait counts stay exact; the weight scales travel with
     // their block instead of being fetched when the epilogue needs them.
     const int nrow = rend - r0;   // rows of this tile (1..32)
     auto load_blk = [&](int b, v4i &A, v4i (&B)[NSUB], float (&S)[NSUB]) {
         const int bc = b < g.nb ? b : g.nb - 1;
-        A = *(const v4i *)(xa + (size_t)bc * BLK);
+        A = *(const __attribute__((address_space(1))) v4i *)(xa + (size_t)bc * BLK);
 #pragma unroll
         for (int s = 0; s < NSUB; ++s) {
             B[s] = load_b<W4>(wp[s] + (size_t)bc * TILE_O * BB);
@@ -164,19 +163,21 @@ __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const i
             }
         }
     };
-    v4i A0, A1, A2;
-    v4i B0[NSUB], B1[NSUB], B2[NSUB];
-    float S0[NSUB], S1[NSUB], S2[NSUB];
-    load_blk(0, A0, B0, S0);
-    load_blk(1, A1, B1, S1);
+    // NS = PD + 1 register slots; the inner loop is fully unrolled so every
+    // slot index is a compile-time constant (registers, not scratch)
+    constexpr int NS = PD + 1;
+    v4i Ar[NS];
+    v4i Br[NS][NSUB];
+    float Sr[NS][NSUB];
+#pragma unroll
+    for (int u = 0; u < PD; ++u) load_blk(u, Ar[u], Br[u], Sr[u]);
 #pragma unroll 1
-    for (int b = 0; b < g.nb; b += 3) {
-        load_blk(b + 2, A2, B2, S2);
-        do_blk(b, A0, B0, S0);
-        load_blk(b + 3, A0, B0, S0);
-        if (b + 1 < g.nb) do_blk(b + 1, A1, B1, S1);
-        load_blk(b + 4, A1, B1, S1);
-        if (b + 2 < g.nb) do_blk(b + 2, A2, B2, S2);
+    for (int b = 0; b < g.nb; b += NS) {
+#pragma unroll
+        for (int u = 0; u < NS; ++u) {
+            load_blk(b + u + PD, Ar[(u + PD) % NS], Br[(u + PD) % NS], Sr[(u + PD) % NS]);
+            if (b + u < g.nb) do_blk(b + u, Ar[u], Br[u], Sr[u]);
+        }
     }
 
     // per-row activation scale (EPI_ROW / EPI_GRP) of each accumulator row
@@ -237,14 +238,19 @@ __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const i
     }
 }
 
-template <bool W4, int EPI, bool GATEUP>
-static void launch_mfma_t(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
+template <bool W4, int EPI, bool GATEUP, int PD>
+static void launch_mfma_p(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
     constexpr int NSUB = 2;
     const int ch_per_wg = GATEUP ? 4 * 32 : 4 * 32 * NSUB;
     const int span = GATEUP ? ((g.O + 31) & ~31) : g.O;
     dim3 grid((unsigned)((span + ch_per_wg - 1) / ch_per_wg), (unsigned)grid_tiles);
     const size_t lds = EPI == EPI_B32 ? (size_t)g.nb * 32 * sizeof(float) : 0;
-    hipLaunchKernelGGL((mfma_kernel<W4, EPI, GATEUP, NSUB>), grid, dim3(256), lds, st, a, g, a.xq, a.sx);
+    hipLaunchKernelGGL((mfma_kernel<W4, EPI, GATEUP, NSUB, PD>), grid, dim3(256), lds, st, a, g, a.xq, a.sx);
+}
+
+template <bool W4, int EPI, bool GATEUP>
+static void launch_mfma_t(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
+    launch_mfma_p<W4, EPI, GATEUP, 2>(a, g, grid_tiles, st);
 }
 
 template <bool GATEUP>

@@ -408,7 +408,7 @@ __global__ __launch_bounds__(1024) void build_table_kernel(const int *ids, int S
                                                            int tmax) {
     __shared__ short sid[TBL_MAXN];
     __shared__ int first[TBL_MAXE], cnt[TBL_MAXE], rank[TBL_MAXE], fill[TBL_MAXE], uex[TBL_MAXE];
-    __shared__ unsigned long long mask[TBL_MAXE];
+    __shared__ unsigned long long mask[TBL_MAXE * 4];   // [e][up to 4 words]: one pass's tokens
     __shared__ int cpos[1024];
     __shared__ int scan_tmp[32];
     __shared__ int s_nu, s_carry[2];
@@ -424,7 +424,7 @@ __global__ __launch_bounds__(1024) void build_table_kernel(const int *ids, int S
     for (int e = tid; e < E; e += nth) {
         first[e] = INT_MAX;
         cnt[e] = 0;
-        mask[e] = 0ull;
+        mask[4 * e] = mask[4 * e + 1] = mask[4 * e + 2] = mask[4 * e + 3] = 0ull;
         rank[e] = -1;
     }
     __syncthreads();
@@ -496,23 +496,29 @@ __global__ __launch_bounds__(1024) void build_table_kernel(const int *ids, int S
         t.hdr[0] = t.hdr[1] = t.hdr[2] = t.hdr[3] = 0;
     }
     __syncthreads();
-    // stable placement, 64 tokens per pass: the rank of an entry among its
-    // expert's rows in this pass = earlier tokens of the pass with the same
-    // expert (a popcount of a per-expert token bitmask)
-    for (int c0 = 0; c0 < S; c0 += 64) {
+    // Stable placement, TPP tokens per pass (one thread per (token, slot)
+    // entry): an entry's rank among its expert's rows in the pass = earlier
+    // tokens of the pass with the same expert, a popcount over the expert's
+    // per-pass token mask (TPP/64 words).
+    const int TPP = min(256, (nth / k) & ~63);   // k <= 16 keeps this >= 64
+    const int W = TPP >> 6;
+    for (int c0 = 0; c0 < S; c0 += TPP) {
         const int i = c0 * k + tid;
-        const bool mine = tid < 64 * k && i < N;
-        int e = -1, bit = 0;
+        const bool mine = tid < TPP * k && i < N;
+        int e = -1, tok = 0;
         if (mine) {
             e = id_at(i);
-            bit = i / k - c0;
-            if (e >= 0) atomicOr(&mask[e], 1ull << bit);
+            tok = i / k - c0;
+            if (e >= 0) atomicOr(&mask[e * 4 + (tok >> 6)], 1ull << (tok & 63));
         }
         __syncthreads();
         if (mine) {
             int r = -1;
             if (e >= 0) {
-                r = fill[e] + __popcll(mask[e] & ((1ull << bit) - 1ull));
+                const unsigned long long *m = &mask[e * 4];
+                int rk = __popcll(m[tok >> 6] & ((1ull << (tok & 63)) - 1ull));
+                for (int w = 0; w < (tok >> 6); w++) rk += __popcll(m[w]);
+                r = fill[e] + rk;
                 t.row_tok[r] = i / k;
                 t.row_kk[r] = i % k;
                 t.row_exp[r] = e;
@@ -521,31 +527,32 @@ __global__ __launch_bounds__(1024) void build_table_kernel(const int *ids, int S
         }
         __syncthreads();
         for (int e2 = tid; e2 < E; e2 += nth) {
-            fill[e2] += __popcll(mask[e2]);
-            mask[e2] = 0ull;
+            int n = 0;
+            for (int w = 0; w < W; w++) {
+                n += __popcll(mask[e2 * 4 + w]);
+                mask[e2 * 4 + w] = 0ull;
+            }
+            fill[e2] += n;
         }
-        // this pass's tokens: rows sorted by union rank (insertion sort, k <= 16)
-        const int s = c0 + tid;
-        if (tid < 64 && s < S) {
-            int rr[16], rk[16], kq[16], j = 0;
-            for (int kk = 0; kk < k; kk++) {
-                const int r = cpos[tid * k + kk];
-                if (r < 0) continue;
-                rr[j] = r;
-                kq[j] = kk;
-                rk[j] = rank[id_at(s * k + kk)];
-                j++;
-            }
-            for (int a = 1; a < j; a++)
-                for (int b = a; b > 0 && rk[b - 1] > rk[b]; b--) {
-                    int tmp = rk[b]; rk[b] = rk[b - 1]; rk[b - 1] = tmp;
-                    tmp = rr[b]; rr[b] = rr[b - 1]; rr[b - 1] = tmp;
-                    tmp = kq[b]; kq[b] = kq[b - 1]; kq[b - 1] = tmp;
+        // the token's rows in union (rank) order: an entry's slot is the
+        // number of the token's valid entries with a lower union rank; the
+        // invalid entries fill the tail in slot order
+        if (mine) {
+            const int sx = i / k, kk = i % k;
+            const int ur = e >= 0 ? rank[e] : INT_MAX;
+            int p = 0, nv = 0, inv_before = 0;
+            for (int k2 = 0; k2 < k; k2++) {
+                const int e2 = id_at(sx * k + k2);
+                if (e2 >= 0) {
+                    nv++;
+                    p += rank[e2] < ur;
+                } else if (k2 < kk) {
+                    inv_before++;
                 }
-            for (int a = 0; a < k; a++) {
-                t.tok_rows[(size_t)s * k + a] = a < j ? rr[a] : -1;
-                t.tok_kk[(size_t)s * k + a] = a < j ? kq[a] : 0;
             }
+            const size_t at = (size_t)sx * k + (e >= 0 ? p : nv + inv_before);
+            t.tok_rows[at] = e >= 0 ? cpos[tid] : -1;
+            t.tok_kk[at] = e >= 0 ? kk : 0;
         }
         __syncthreads();
     }

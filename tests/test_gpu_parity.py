@@ -389,3 +389,23 @@ def test_golden_layer_bit_exact(hip, arm):
         assert np.array_equal(bids.download(np.int32, (S, k)), f["ids"])
         assert bw.download(np.float32, (S, k)).tobytes() == f["w"].tobytes()
         assert bout.download(np.float32, (S, D)).tobytes() == f[f"y_ga{ga}"].tobytes(), ga
+
+
+@pytest.mark.parametrize("S,k,E", [(600, 8, 40), (300, 16, 24), (1100, 1, 12)])
+def test_expert_table_many_passes(hip, orc, S, k, E):
+    """The device-built expert-offset table for batches that take several
+    placement passes (and multi-word token masks) equals the oracle's, and the
+    layer output stays bit-identical."""
+    say("table many passes", S, k, E)
+    rng = np.random.default_rng(900 + S + k)
+    D, I = 64, 32
+    gpu, ora, eset, x, logits = _layer_case(hip, orc, rng, E, D, I, S, k, zipf=True)
+    out, ids, w = _run_layer(hip, eset, x, logits, k, 32, 0)
+    t = hip.last_table(0, E, S * k)
+    o = orc.expert_table(ids, E)
+    assert t["n_u"] == o["n_u"] and np.array_equal(t["uexp"], o["uexp"]) and np.array_equal(t["off"], o["off"])
+    assert np.array_equal(t["row_tok"], o["row_tok"])
+    assert np.array_equal(t["tok_rows"].reshape(S, k), o["tok_rows"])
+    sub = np.arange(0, S, max(1, S // 40))
+    ref = orc.moe_forward(x, ids, w, ora, 32, subset=sub, nthreads=8)
+    assert np.array_equal(out[sub], ref[sub])
