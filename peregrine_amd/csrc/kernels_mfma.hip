@@ -114,70 +114,92 @@ __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const i
             if constexpr (EPI != EPI_ROW) S[s] = sp[s][(size_t)grp_of(bc, g.gshift) * TILE_O];
         }
     };
-    auto do_blk = [&](int b, const v4i &A, const v4i (&B)[NSUB], const float (&S)[NSUB]) {
-        const bool gend = grp_end(b, g.gshift, g.nb);
+    // Each block: the MFMAs (integer dots), then the f32 epilogue. The loop
+    // issues block b+1's MFMAs before block b's epilogue, so the matrix cores
+    // run under the VALU epilogue. A block that opens a weight group starts
+    // its MFMA accumulation from zero; the int32 result of a block that
+    // closes one is the group's exact dot.
+    auto mma_blk = [&](int b, const v4i &A, const v4i (&B)[NSUB], v16i (&D)[NSUB]) {
+        const bool opens = EPI == EPI_B32 || (EPI == EPI_GRP && (b == 0 || grp_end(b - 1, g.gshift, g.nb))) ||
+                           (EPI == EPI_ROW && b == 0);
 #pragma unroll
         for (int s = 0; s < NSUB; ++s) {
-            const v16i cin = (EPI == EPI_B32) ? v16i{} : iacc[s];
-            const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B[s], cin, 0, 0, 0);
+            const v16i cin = opens ? v16i{} : iacc[s];
+            D[s] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B[s], cin, 0, 0, 0);
+            if (EPI != EPI_B32) iacc[s] = D[s];
             if (a.dots) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const int row = r0 + acc_row(i, lane);
-                    const int val = d[i] - (EPI == EPI_B32 ? 0 : cin[i]);
+                    const int val = D[s][i] - cin[i];
                     if (row < rend && oc[s] < g.O)
                         a.dots[(((size_t)row * (GATEUP ? 2 : 1) + (GATEUP ? s : 0)) * g.O + oc[s]) * g.nb + b] =
                             W4 ? (val >> 4) : val;
                 }
             }
-            if constexpr (EPI == EPI_ROW) {
-                iacc[s] = d;
-            } else if constexpr (EPI == EPI_GRP) {
-                if (gend) {
+        }
+    };
+    auto epi_blk = [&](int b, const v16i (&D)[NSUB], const float (&S)[NSUB]) {
+        if constexpr (EPI == EPI_ROW) return;   // integer sum to the end
+        if (EPI == EPI_GRP && !grp_end(b, g.gshift, g.nb)) return;
+        if constexpr (EPI == EPI_B32) {
+            const float4 *sx4 = (const float4 *)(sxl + b * 32 + 4 * hh);
 #pragma unroll
-                    for (int gq = 0; gq < 4; ++gq) {
-                        if (8 * gq >= nrow) break;   // uniform: rows past the tile's end
+            for (int gq = 0; gq < 4; ++gq) {
+                if (8 * gq >= nrow) break;   // uniform: rows past the tile's end
+                const float4 sq = sx4[2 * gq];
+                const float sxr[4] = {sq.x, sq.y, sq.z, sq.w};
 #pragma unroll
-                        for (int t = 0; t < 4; ++t) {
-                            const int i = 4 * gq + t;
-                            acc[s][i] = __fadd_rn(acc[s][i], __fmul_rn((float)d[i], S[s]));
-                        }
-                    }
-                    iacc[s] = v16i{};
-                } else {
-                    iacc[s] = d;
-                }
-            } else {
-                const float4 *sx4 = (const float4 *)(sxl + b * 32 + 4 * hh);
-#pragma unroll
-                for (int gq = 0; gq < 4; ++gq) {
-                    if (8 * gq >= nrow) break;   // uniform: rows past the tile's end
-                    const float4 sq = sx4[2 * gq];
-                    const float sxr[4] = {sq.x, sq.y, sq.z, sq.w};
+                for (int s = 0; s < NSUB; ++s) {
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
                         const int i = 4 * gq + t;
-                        acc[s][i] = __fmaf_rn(__fmul_rn(S[s], sxr[t]), (float)d[i], acc[s][i]);
+                        acc[s][i] = __fmaf_rn(__fmul_rn(S[s], sxr[t]), (float)D[s][i], acc[s][i]);
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+                if (8 * gq >= nrow) break;
+#pragma unroll
+                for (int s = 0; s < NSUB; ++s) {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const int i = 4 * gq + t;
+                        acc[s][i] = __fadd_rn(acc[s][i], __fmul_rn((float)D[s][i], S[s]));
                     }
                 }
             }
         }
     };
-    // NS = PD + 1 register slots; the inner loop is fully unrolled so every
-    // slot index is a compile-time constant (registers, not scratch)
-    constexpr int NS = PD + 1;
+    // PD + 1 = 3 operand slots and two MFMA-result buffers rotate through a
+    // loop unrolled by six, so every index is a compile-time constant:
+    // iteration u refills the slot block u-1 has released with block u + PD,
+    // issues block u's MFMAs, then runs block u-1's epilogue.
+    static_assert(PD == 2, "slot rotation assumes three slots");
+    constexpr int NS = PD + 1, NU = 6;
     v4i Ar[NS];
     v4i Br[NS][NSUB];
     float Sr[NS][NSUB];
+    v16i Dr[2][NSUB];
 #pragma unroll
     for (int u = 0; u < PD; ++u) load_blk(u, Ar[u], Br[u], Sr[u]);
 #pragma unroll 1
-    for (int b = 0; b < g.nb; b += NS) {
+    for (int b = 0; b < g.nb; b += NU) {
 #pragma unroll
-        for (int u = 0; u < NS; ++u) {
-            load_blk(b + u + PD, Ar[(u + PD) % NS], Br[(u + PD) % NS], Sr[(u + PD) % NS]);
-            if (b + u < g.nb) do_blk(b + u, Ar[u], Br[u], Sr[u]);
+        for (int u = 0; u < NU; ++u) {
+            const int cur = u % NS, prev = (u + NS - 1) % NS;
+            float Sp[NSUB];   // block u-1's scales: its slot is refilled first
+#pragma unroll
+            for (int s = 0; s < NSUB; ++s) Sp[s] = Sr[prev][s];
+            load_blk(b + u + PD, Ar[prev], Br[prev], Sr[prev]);
+            if (b + u < g.nb) mma_blk(b + u, Ar[cur], Br[cur], Dr[u & 1]);
+            if (b + u > 0 && b + u - 1 < g.nb) epi_blk(b + u - 1, Dr[(u + 1) & 1], Sp);
         }
+    }
+    if (g.nb % NU == 0) {   // the last block's epilogue did not run inside the loop
+        epi_blk(g.nb - 1, Dr[(NU - 1) & 1], Sr[(NU - 1) % NS]);
     }
 
     // per-row activation scale (EPI_ROW / EPI_GRP) of each accumulator row
