@@ -173,12 +173,11 @@ __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const i
             }
         }
     };
-    // PD + 1 = 3 operand slots and two MFMA-result buffers rotate through a
-    // loop unrolled by six, so every index is a compile-time constant:
+    // PD + 1 operand slots and two MFMA-result buffers rotate through a loop
+    // unrolled by a multiple of both, so every index is a compile-time constant:
     // iteration u refills the slot block u-1 has released with block u + PD,
     // issues block u's MFMAs, then runs block u-1's epilogue.
-    static_assert(PD == 2, "slot rotation assumes three slots");
-    constexpr int NS = PD + 1, NU = 6;
+    constexpr int NS = PD + 1, NU = NS % 2 ? 2 * NS : NS;   // unroll: a multiple of both rotations
     v4i Ar[NS];
     v4i Br[NS][NSUB];
     float Sr[NS][NSUB];
@@ -272,7 +271,7 @@ static void launch_mfma_p(const DotArgs &a, const MatGeom &g, int grid_tiles, hi
 
 template <bool W4, int EPI, bool GATEUP>
 static void launch_mfma_t(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
-    launch_mfma_p<W4, EPI, GATEUP, 2>(a, g, grid_tiles, st);
+    launch_mfma_p<W4, EPI, GATEUP, 2>(a, g, grid_tiles, st);   // two blocks ahead: deeper costs occupancy
 }
 
 template <bool GATEUP>
