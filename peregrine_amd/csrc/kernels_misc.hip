@@ -2,6 +2,8 @@
 // device router, the expert-offset table and the fixed-order combine.
 #include <climits>
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace phip {
@@ -158,20 +160,53 @@ __global__ __launch_bounds__(256) void combine_csr_kernel(float *out, const floa
 // Device-table form: token s adds its rows tok_rows[s*k + j] (union order,
 // -1 terminates) weighted by w[s*k + tok_kk[s*k + j]] — the reference scatter
 // out[s] += w * y (mlp.rs:111-119) from a zero row.
+// out[s] = sum over the token's rows in batch-union order of w * y[row]
+// (mul then add, from 0). Four channels per thread; the token's row indices
+// and weights are the same for the whole workgroup (scalar loads), and every
+// y load is issued before the in-order sum.
 __global__ __launch_bounds__(256) void combine_tok_kernel(float *out, const float *y, const int *tok_rows,
                                                           const int *tok_kk, const float *w, int k, int D,
-                                                          int y_stride) {
+                                                          int y_stride, int vec4) {
     const int s = blockIdx.y;
-    const int d = blockIdx.x * 256 + threadIdx.x;
-    if (d >= D) return;
-    float acc = 0.0f;
-    for (int j = 0; j < k; j++) {
-        const int r = tok_rows ? tok_rows[(size_t)s * k + j] : j;
-        if (r < 0) break;
-        const float wt = w[(size_t)s * k + (tok_kk ? tok_kk[(size_t)s * k + j] : j)];
-        acc = __fadd_rn(acc, __fmul_rn(wt, y[(size_t)r * y_stride + d]));
+    const int d0 = (blockIdx.x * 256 + threadIdx.x) * 4;
+    int rr[16];
+    float ww[16];
+    int n = 0;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        if (j < k && n == j) {
+            const int r = tok_rows ? tok_rows[(size_t)s * k + j] : j;
+            if (r >= 0) {
+                rr[j] = r;
+                ww[j] = w[(size_t)s * k + (tok_kk ? tok_kk[(size_t)s * k + j] : j)];
+                n = j + 1;
+            }
+        }
     }
-    out[(size_t)s * D + d] = acc;
+    if (d0 >= D) return;
+    if (vec4) {   // D and the row strides are multiples of 4
+        float4 yv[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++)
+            if (j < n) yv[j] = *(const float4 *)(y + (size_t)rr[j] * y_stride + d0);
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            if (j < n) {
+                acc.x = __fadd_rn(acc.x, __fmul_rn(ww[j], yv[j].x));
+                acc.y = __fadd_rn(acc.y, __fmul_rn(ww[j], yv[j].y));
+                acc.z = __fadd_rn(acc.z, __fmul_rn(ww[j], yv[j].z));
+                acc.w = __fadd_rn(acc.w, __fmul_rn(ww[j], yv[j].w));
+            }
+        }
+        *(float4 *)(out + (size_t)s * D + d0) = acc;
+    } else {
+        for (int d = d0; d < min(D, d0 + 4); d++) {
+            float acc = 0.0f;
+            for (int j = 0; j < n; j++) acc = __fadd_rn(acc, __fmul_rn(ww[j], y[(size_t)rr[j] * y_stride + d]));
+            out[(size_t)s * D + d] = acc;
+        }
+    }
 }
 
 void launch_combine(float *out, const float *y, const int *row_ptr, const int *row_idx, const float *rw, int s_n,
@@ -184,8 +219,9 @@ void launch_combine(float *out, const float *y, const int *row_ptr, const int *r
 void launch_combine_tok(float *out, const float *y, const int *tok_rows, const int *tok_kk, const float *w, int s_n,
                         int k, int D, int y_stride, hipStream_t st) {
     if (s_n <= 0) return;
-    hipLaunchKernelGGL(combine_tok_kernel, dim3((unsigned)((D + 255) / 256), (unsigned)s_n), dim3(256), 0, st, out,
-                       y, tok_rows, tok_kk, w, k, D, y_stride);
+    const int vec4 = (D % 4 == 0 && y_stride % 4 == 0) ? 1 : 0;
+    hipLaunchKernelGGL(combine_tok_kernel, dim3((unsigned)((D + 1023) / 1024), (unsigned)s_n), dim3(256), 0, st, out,
+                       y, tok_rows, tok_kk, w, k, D, y_stride, vec4);
 }
 
 // ---------------------------------------------------------------------------
@@ -302,16 +338,37 @@ __global__ __launch_bounds__(256) void route_quant_kernel(const float *logits, i
     const float *x = a.x + (size_t)s * a.x_stride;
     int8_t *q = a.q + (size_t)s * a.q_stride;
     if (a.mode == ACT_B32) {
-        const int b = blockIdx.y * 8 + (tid >> 5), l32 = tid & 31;
-        if (b * BLK >= a.Kp) return;
-        const int kx = b * BLK + l32;
-        const float v = kx < a.K ? x[kx] : 0.0f;
-        const float m = warp_max(fabsf(v), 32);
-        float sc = __fdiv_rn(m, 127.0f);
-        if (sc < 1e-12f) sc = 1e-12f;
-        const float inv = __fdiv_rn(1.0f, sc);
-        q[perm8(kx)] = (int8_t)(int)rintf(__fmul_rn(v, inv));
-        if (l32 == 0) a.s[(size_t)s * a.s_stride + b] = sc;
+        // this slab's 32-blocks; 8 lanes per block, 4 elements per lane, a
+        // workgroup covers 32 blocks per step
+        const int nbk = a.Kp / BLK;
+        const int per = (nbk + (int)gridDim.y - 1) / (int)gridDim.y;
+        const int b_lo = blockIdx.y * per, b_hi = min(nbk, b_lo + per);
+        const int sub = lane & 7;
+        for (int b = b_lo + wave * 8 + (lane >> 3); b - (wave * 8 + (lane >> 3)) < b_hi; b += 32) {
+            const bool ok = b < b_hi;   // the same for the 8 lanes of a block
+            float v[4];
+            float m = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int kx = b * BLK + sub * 4 + t;
+                v[t] = ok && kx < a.K ? x[kx] : 0.0f;
+                m = fmaxf(m, fabsf(v[t]));
+            }
+            m = fmaxf(m, __shfl_xor(m, 1));
+            m = fmaxf(m, __shfl_xor(m, 2));
+            m = fmaxf(m, __shfl_xor(m, 4));
+            float sc = __fdiv_rn(m, 127.0f);
+            if (sc < 1e-12f) sc = 1e-12f;
+            const float inv = __fdiv_rn(1.0f, sc);
+            if (ok) {
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const int kx = b * BLK + sub * 4 + t;
+                    q[perm8(kx)] = (int8_t)(int)rintf(__fmul_rn(v[t], inv));
+                }
+                if (sub == 0) a.s[(size_t)s * a.s_stride + b] = sc;
+            }
+        }
     } else {
         constexpr int PX = 32;   // K <= 8192 from registers, the rest re-read
         float v[PX];
@@ -346,7 +403,10 @@ __global__ __launch_bounds__(256) void route_quant_kernel(const float *logits, i
 template <int PER>
 static void route_quant_t(const float *logits, int S, int E, int k, int *ids, float *w, const QuantArgs &a,
                           const ExpertDesc *desc, ExpertDesc *row_desc, hipStream_t st) {
-    const int slabs = a.mode == ACT_B32 ? (a.Kp / BLK + 7) / 8 : 1;
+    // few tokens: spread a row over several workgroups (8 blocks each at one
+    // token); many tokens: one workgroup per token
+    const int nbk = a.Kp / BLK;
+    const int slabs = a.mode == ACT_B32 ? std::max(1, std::min((nbk + 7) / 8, 256 / S)) : 1;
     hipLaunchKernelGGL(route_quant_kernel<PER>, dim3((unsigned)S, (unsigned)slabs), dim3(256), 0, st, logits, E, k,
                        ids, w, a, desc, row_desc);
 }
