@@ -218,7 +218,6 @@ struct DotArgs {   // shared by the GEMV and MFMA arms
     int act_zero;                                                       // activation row = 0 (one token)
     int n_rows_fixed;                                                   // >= 0: row count known on the host
     long long *trace;                                                   // optional phase timestamps (tests/tuning)
-    int buf_ok;   // every expert's gate/up tiles lie within one 4 GB buffer window
 };
 // grid_rows / grid_tiles: host-side upper bounds; the kernels read the true
 // counts from plan.counts and idle the excess workgroups.

@@ -41,7 +41,6 @@ struct ColiHipExpertSet {
     int device, count;
     MatGeom gg, gd;          // gate/up geometry, down geometry
     ExpertDesc *desc_dev;    // [count]
-    int buf_ok;              // gate/up pairs fit one 4 GB buffer window
 };
 
 namespace {
@@ -363,24 +362,6 @@ int upload_impl(ColiHipTensor **tensor, const void *weights, const float *scales
 
 int epi_act(int ga) { return ga == 32 ? ACT_B32 : ACT_ROW; }
 
-// Whether the gate and up tensors of one expert can be addressed from a
-// single buffer descriptor (distance + size below 2 GB, for weights and scales).
-bool pair_in_window(const ColiHipTensor *g, const ColiHipTensor *u) {
-    const auto span = [](const void *a, const void *b, size_t n) {
-        const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
-        return (x > y ? x - y : y - x) + n;
-    };
-    const size_t lim = (size_t)1 << 31;
-    return span(g->w, u->w, std::max(g->w_bytes, u->w_bytes)) < lim &&
-           span(g->sc, u->sc, std::max(g->sc_bytes, u->sc_bytes)) < lim;
-}
-
-int group_buf_ok(ColiHipTensor *const *gates, ColiHipTensor *const *ups, int count) {
-    for (int c = 0; c < count; c++)
-        if (!pair_in_window(gates[c], ups[c])) return 0;
-    return 1;
-}
-
 // Validate a gate/up/down triple list; fills the two geometries.
 int check_group(ColiHipTensor *const *gates, ColiHipTensor *const *ups, ColiHipTensor *const *downs, int count,
                 int *device, MatGeom *gg, MatGeom *gd) {
@@ -473,7 +454,6 @@ int reserve_rows(Ctx *c, const MatGeom &gg, const MatGeom &gd, int rows_x, int R
 struct DispatchOpts {
     bool x_quantized = false;   // xq/sx already written (fused router + quant)
     bool act_zero = false;      // every row reads activation row 0 (one token)
-    int buf_ok = 0;             // gate/up pairs fit one buffer descriptor
     int n_rows_fixed = -1;      // row count known on the host
 };
 
@@ -507,7 +487,6 @@ void run_experts(Ctx *c, Prof &prof, const ExpertDesc *desc, const RowPlan &plan
     da.act_identity = x_identity ? 1 : 0;
     da.act_zero = opt.act_zero ? 1 : 0;
     da.n_rows_fixed = opt.n_rows_fixed;
-    da.buf_ok = opt.buf_ok;
     prof.mark(COLI_HIP_K_GATEUP);
     if (arm == COLI_HIP_ARM_GEMV)
         launch_gemv_gateup(da, gg, act, R_bound, c->stream);
@@ -644,7 +623,6 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
     plan.mt_rend = di + total + 2 * T;
     plan.counts = di + total + 3 * T;
     DispatchOpts opt;
-    opt.buf_ok = group_buf_ok(gates, ups, count);
     run_experts(c, prof, (const ExpertDesc *)dm, plan, gg, gd, x_dev, total, true, total, T, ga, arm, s, opt);
     float *res = s.y;
     if (red) {
@@ -1010,7 +988,6 @@ int coli_hip_expert_set_create(ColiHipExpertSet **set, ColiHipTensor *const *gat
     s->count = count;
     s->gg = gg;
     s->gd = gd;
-    s->buf_ok = group_buf_ok(gates, ups, count);
     if (!hip_ok(hipMalloc(&s->desc_dev, sizeof(ExpertDesc) * count), "expert set allocation") ||
         !hip_ok(hipMemcpy(s->desc_dev, hd.data(), sizeof(ExpertDesc) * count, hipMemcpyHostToDevice),
                 "expert set upload")) {
@@ -1092,7 +1069,6 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
 
     Prof prof(c);
     DispatchOpts opt;
-    opt.buf_ok = set->buf_ok;
     const int act = epi_act(ga);
     // one token routes to k distinct experts in top-k order, which is also
     // batch-union order: row r is (token 0, slot r) and no table is needed

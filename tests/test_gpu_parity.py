@@ -299,10 +299,14 @@ def test_batched_layer_full_width_sampled(hip, orc):
     assert nerr(out[sub], ref[sub]) <= TOL
 
 
-def test_graph_replay_matches_eager(hip, orc):
-    say("graph replay")
-    rng = np.random.default_rng(91)
-    E, D, I, S, k = 8, 256, 128, 3, 2
+@pytest.mark.parametrize("S", [3, 1])
+def test_graph_replay_matches_eager(hip, orc, S):
+    """Replays of a captured layer equal eager runs (S = 1 exercises the
+    one-token path, whose down projection also combines through per-tile
+    counters that must rearm between replays)."""
+    say("graph replay", S)
+    rng = np.random.default_rng(91 + S)
+    E, D, I, k = 8, 256, 128, 2
     gpu, ora, eset, x, logits = _layer_case(hip, orc, rng, E, D, I, S, k)
     bx = hip.DeviceBuffer.from_array(x)
     bl = hip.DeviceBuffer.from_array(logits)
