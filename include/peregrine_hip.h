@@ -131,6 +131,15 @@ void coli_hip_expert_set_free(ColiHipExpertSet *set);
  * stream. */
 int coli_hip_route_softmax_topk_dev(int device, const float *logits_dev, int S, int E, int k, int *ids_dev,
                                     float *w_dev);
+/* The reference's router on the device (router.rs:52-170 after the router
+ * matmul; the reference runs it on the host): sigmoid scores, greedy top-k
+ * over score + bias[e] (bias_dev may be NULL: zero), weight = the sigmoid,
+ * unfilled slots (0, 0), the negligible tail dropped when min_share > 0
+ * (router.rs:191-209), optional renormalisation (+1e-20), times routed_scale.
+ * keff_dev[S] (may be NULL) receives each token's kept count. Async. */
+int coli_hip_route_sigmoid_topk_dev(int device, const float *logits_dev, const float *bias_dev, int S, int E, int k,
+                                    int norm_topk, float routed_scale, float min_share, int *ids_dev, float *w_dev,
+                                    int *keff_dev);
 /* One routed MoE layer: out[S][D] = sum over each token's k experts, in
  * batch-union order, of w * SwiGLU_e(x). ids/w are [S][k] (device). act_group
  * 0 or 32; arm -1 automatic. The expert-offset table is built on the device.

@@ -268,13 +268,31 @@ static int greedy_topk(const float *score, int e_n, int k, int32_t *ib) {
     return k;
 }
 
-/* route — crates/peregrine-model/src/router.rs:52-170 with min_share = 0
- * (negligible_tail off), taking the router logits as input (the router matmul
- * is orc_matmul_f32). sigmoid scores, selection by sigmoid + bias, weight = the
- * plain sigmoid, optional renormalisation over all k slots (+1e-20), then
- * routed_scale. Returns 0. */
+/* negligible_tail — router.rs:191-209: how many trailing kept weights carry
+ * less than min_share of the kept sum (scanned from the end, stopping at the
+ * first one that does not; at most kept-1; none for a degenerate sum). */
+int orc_negligible_tail(const float *w, int kept, float min_share) {
+    if (min_share <= 0.0f || kept <= 1) return 0;
+    float sum = 0.0f;
+    for (int i = 0; i < kept; i++) sum += w[i];
+    if (!isfinite(sum) || sum <= 0.0f) return 0;
+    int drop = 0;
+    while (drop < kept - 1) {
+        const int i = kept - 1 - drop;
+        if (w[i] / sum >= min_share) break;
+        drop++;
+    }
+    return drop;
+}
+
+/* route — crates/peregrine-model/src/router.rs:52-170 (after the router
+ * matmul): sigmoid scores, greedy top-k over score + bias (strict >, ties to
+ * the lowest index, NaN never picked), weight = the sigmoid; unfilled slots
+ * (0, 0); the negligible tail dropped (min_share > 0); optional renormalise
+ * over all k slots with +1e-20; times routed_scale. sigmoid = 1/(1+exp(-x))
+ * with exp evaluated as exp_cr. */
 int orc_route_sigmoid(const float *logits, const float *bias, int s_n, int e_n, int k, int norm_topk,
-                      float routed_scale, int32_t *idx, float *w, int32_t *keff) {
+                      float routed_scale, float min_share, int32_t *idx, float *w, int32_t *keff) {
     float *sig = malloc(sizeof(float) * e_n), *choice = malloc(sizeof(float) * e_n);
     for (int s = 0; s < s_n; s++) {
         for (int e = 0; e < e_n; e++) {
@@ -286,6 +304,9 @@ int orc_route_sigmoid(const float *logits, const float *bias, int s_n, int e_n, 
         int kept = greedy_topk(choice, e_n, k, ib);
         for (int kk = 0; kk < kept; kk++) wb[kk] = sig[ib[kk]];
         for (int kk = kept; kk < k; kk++) { ib[kk] = 0; wb[kk] = 0.0f; }
+        const int drop = orc_negligible_tail(wb, kept, min_share);
+        for (int kk = kept - drop; kk < kept; kk++) { ib[kk] = 0; wb[kk] = 0.0f; }
+        kept -= drop;
         keff[s] = kept;
         if (norm_topk) {
             float sm = 0.0f;

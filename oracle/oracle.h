@@ -59,8 +59,9 @@ void orc_expert_swiglu(float *y, const float *x, int S, const OrcTensor *gate, c
                        const OrcTensor *down, int ga, float *h_out);
 
 /* ---- routing ---- */
+int orc_negligible_tail(const float *w, int kept, float min_share);
 int orc_route_sigmoid(const float *logits, const float *bias, int s_n, int e_n, int k, int norm_topk,
-                      float routed_scale, int32_t *idx, float *w, int32_t *keff);
+                      float routed_scale, float min_share, int32_t *idx, float *w, int32_t *keff);
 void orc_route_softmax_topk(const float *logits, int s_n, int e_n, int k, int32_t *idx, float *w);
 int orc_batch_union(const int32_t *idx, const int32_t *keff, int s_n, int k, int e_n, int32_t *uniq);
 

@@ -69,7 +69,8 @@ _silu_mul = _sig("orc_silu_mul", None, _f32p, _f32p, C.c_int)
 _swiglu = _sig("orc_expert_swiglu", None, _f32p, _f32p, C.c_int, C.POINTER(_OrcTensor),
                C.POINTER(_OrcTensor), C.POINTER(_OrcTensor), C.c_int, C.c_void_p)
 _route_sig = _sig("orc_route_sigmoid", C.c_int, _f32p, _f32p, C.c_int, C.c_int, C.c_int, C.c_int,
-                  C.c_float, _i32p, _f32p, _i32p)
+                  C.c_float, C.c_float, _i32p, _f32p, _i32p)
+_neg_tail = _sig("orc_negligible_tail", C.c_int, _f32p, C.c_int, C.c_float)
 _route_smx = _sig("orc_route_softmax_topk", None, _f32p, C.c_int, C.c_int, C.c_int, _i32p, _f32p)
 _union = _sig("orc_batch_union", C.c_int, _i32p, C.c_void_p, C.c_int, C.c_int, C.c_int, _i32p)
 _table = _sig("orc_expert_table", C.c_int, _i32p, C.c_int, C.c_int, C.c_int, _i32p, _i32p, _i32p,
@@ -188,14 +189,18 @@ def expert_swiglu(x, gate: Tensor, up: Tensor, down: Tensor, ga=0, want_h=False)
     return (y, h) if want_h else y
 
 
-def route_sigmoid(logits, bias, k, norm_topk=True, routed_scale=1.0):
+def route_sigmoid(logits, bias, k, norm_topk=True, routed_scale=1.0, min_share=0.0):
     logits = _c(logits, np.float32)
     s_n, e_n = logits.shape
     idx = np.zeros((s_n, k), np.int32)
     w = np.zeros((s_n, k), np.float32)
     keff = np.zeros(s_n, np.int32)
-    _route_sig(logits, _c(bias, np.float32), s_n, e_n, k, int(norm_topk), routed_scale, idx, w, keff)
+    _route_sig(logits, _c(bias, np.float32), s_n, e_n, k, int(norm_topk), routed_scale, min_share, idx, w, keff)
     return idx, w, keff
+
+
+def negligible_tail(w, kept, min_share):
+    return int(_neg_tail(_c(w, np.float32), kept, min_share))
 
 
 def route_softmax_topk(logits, k):

@@ -231,6 +231,8 @@ void launch_combine(float *out, const float *y, const int *row_ptr, const int *r
 void launch_combine_tok(float *out, const float *y, const int *tok_rows, const int *tok_kk, const float *w, int s_n,
                         int k, int D, int y_stride, hipStream_t st);
 void launch_route_softmax(const float *logits, int S, int E, int k, int *ids, float *w, hipStream_t st);
+void launch_route_sigmoid(const float *logits, const float *bias, int S, int E, int k, int norm_topk,
+                          float routed_scale, float min_share, int *ids, float *w, int *keff, hipStream_t st);
 void launch_route_quant(const float *logits, int S, int E, int k, int *ids, float *w, const QuantArgs &a,
                         const ExpertDesc *desc, ExpertDesc *row_desc, hipStream_t st);
 // LDS bytes one workgroup may use (device attribute), set at init.

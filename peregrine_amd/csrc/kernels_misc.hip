@@ -315,6 +315,107 @@ __device__ void route_token(const float *l, int E, int k, int *ids, float *w, co
     }
 }
 
+// The reference's own router (peregrine-model/src/router.rs:52-170, after
+// the router matmul), one wavefront per token: sigmoid scores (exp evaluated
+// as exp_cr), greedy top-k over score + bias with the same argmax rounds,
+// weight = the winner's sigmoid; unfilled slots (0, 0); the negligible tail
+// (router.rs:191-209) dropped when min_share > 0; optional renormalisation
+// over all k slots (+1e-20, summed in slot order); times routed_scale.
+template <int PER>
+__global__ __launch_bounds__(64) void route_sigmoid_kernel(const float *logits, const float *bias, int E, int k,
+                                                           int norm_topk, float routed_scale, float min_share,
+                                                           int *ids_out, float *w_out, int *keff_out) {
+    const int s = blockIdx.x, lane = threadIdx.x & 63;
+    const float *l = logits + (size_t)s * E;
+    float ve[PER], sg[PER];
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int e = lane + 64 * j;
+        float c = -INFINITY, sig = 0.0f;
+        if (e < E) {
+            sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, exp_cr(-l[e])));
+            c = __fadd_rn(sig, bias ? bias[e] : 0.0f);
+        }
+        sg[j] = sig;
+        ve[j] = c > -INFINITY ? c : -INFINITY;   // NaN and -inf never qualify
+    }
+    float myw = 0.0f;
+    int myid = 0, kept = 0;
+    for (int kk = 0; kk < k; kk++) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < PER; j++)
+            if (ve[j] > bv) {
+                bv = ve[j];
+                bi = lane + 64 * j;
+            }
+        wave_argmax(bv, bi);
+        if (!(bv > -INFINITY)) break;   // uniform: nothing valid remains
+        float cand = 0.0f;
+#pragma unroll
+        for (int j = 0; j < PER; j++)
+            if (j == (bi >> 6)) cand = sg[j];
+        const float wsel = __shfl(cand, bi & 63);   // the winner's sigmoid
+        if (lane == kk) {
+            myw = wsel;
+            myid = bi;
+        }
+        if ((bi & 63) == lane) {
+#pragma unroll
+            for (int j = 0; j < PER; j++)
+                if (j == (bi >> 6)) ve[j] = -INFINITY;
+        }
+        kept++;
+    }
+    // negligible tail: a trailing run of kept weights under min_share of the
+    // kept sum, at most kept - 1 (every lane computes the same, uniformly)
+    int drop = 0;
+    if (min_share > 0.0f && kept > 1) {
+        float sum = 0.0f;
+        for (int i = 0; i < kept; i++) sum = __fadd_rn(sum, __shfl(myw, i));
+        if (isfinite(sum) && sum > 0.0f) {
+            while (drop < kept - 1) {
+                const float wi = __shfl(myw, kept - 1 - drop);
+                if (__fdiv_rn(wi, sum) >= min_share) break;
+                drop++;
+            }
+        }
+    }
+    kept -= drop;
+    if (lane >= kept) {
+        myw = 0.0f;
+        myid = 0;
+    }
+    if (norm_topk) {
+        float sm = 0.0f;
+        for (int i = 0; i < k; i++) sm = __fadd_rn(sm, __shfl(myw, i));
+        sm = __fadd_rn(sm, 1e-20f);
+        myw = __fdiv_rn(myw, sm);
+    }
+    myw = __fmul_rn(myw, routed_scale);
+    if (lane < k) {
+        ids_out[(size_t)s * k + lane] = myid;
+        w_out[(size_t)s * k + lane] = myw;
+    }
+    if (lane == 0 && keff_out) keff_out[s] = kept;
+}
+
+void launch_route_sigmoid(const float *logits, const float *bias, int S, int E, int k, int norm_topk,
+                          float routed_scale, float min_share, int *ids, float *w, int *keff, hipStream_t st) {
+    if (S <= 0) return;
+    const dim3 g((unsigned)S), b(64);
+#define PHIP_ROUTE_SIG(P) \
+    hipLaunchKernelGGL(route_sigmoid_kernel<P>, g, b, 0, st, logits, bias, E, k, norm_topk, routed_scale, min_share, \
+                       ids, w, keff)
+    if (E <= 64) PHIP_ROUTE_SIG(1);
+    else if (E <= 128) PHIP_ROUTE_SIG(2);
+    else if (E <= 256) PHIP_ROUTE_SIG(4);
+    else if (E <= 512) PHIP_ROUTE_SIG(8);
+    else PHIP_ROUTE_SIG(16);
+#undef PHIP_ROUTE_SIG
+}
+
 template <int PER>
 __global__ __launch_bounds__(64) void route_softmax_kernel(const float *logits, int E, int k, int *ids, float *w) {
     const int s = blockIdx.x;

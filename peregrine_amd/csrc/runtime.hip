@@ -1007,6 +1007,18 @@ void coli_hip_expert_set_free(ColiHipExpertSet *s) {
     std::free(s);
 }
 
+int coli_hip_route_sigmoid_topk_dev(int device, const float *logits_dev, const float *bias_dev, int S, int E, int k,
+                                    int norm_topk, float routed_scale, float min_share, int *ids_dev, float *w_dev,
+                                    int *keff_dev) {
+    Ctx *c = find_ctx(device);
+    if (!logits_dev || !ids_dev || !w_dev || S < 1 || E < 1 || E > 1024 || k < 1 || k > 16 || k > E ||
+        !select_ctx(c))
+        return 0;
+    launch_route_sigmoid(logits_dev, bias_dev, S, E, k, norm_topk, routed_scale, min_share, ids_dev, w_dev, keff_dev,
+                         c->stream);
+    return hip_ok(hipGetLastError(), "sigmoid router launch");
+}
+
 int coli_hip_route_softmax_topk_dev(int device, const float *logits_dev, int S, int E, int k, int *ids_dev,
                                     float *w_dev) {
     Ctx *c = find_ctx(device);

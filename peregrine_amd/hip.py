@@ -376,6 +376,18 @@ def route_softmax_topk_dev(device, logits_ptr, S, E, k, ids_ptr, w_ptr):
         raise HipError("hip route_softmax_topk failed")
 
 
+def route_sigmoid_topk_dev(device, logits_ptr, bias_ptr, S, E, k, ids_ptr, w_ptr, keff_ptr=0, norm_topk=True,
+                           routed_scale=1.0, min_share=0.0):
+    """router.rs:52-170 on the device (async): sigmoid scores, top-k over
+    score + bias (bias_ptr 0: none), weights = sigmoid, tail drop, renorm,
+    routed_scale; keff_ptr (optional) receives the kept counts."""
+    if lib.coli_hip_route_sigmoid_topk_dev(device, C.c_void_p(logits_ptr), C.c_void_p(bias_ptr or None), S, E, k,
+                                           int(norm_topk), float(routed_scale), float(min_share),
+                                           C.c_void_p(ids_ptr), C.c_void_p(w_ptr),
+                                           C.c_void_p(keff_ptr or None)) != 1:
+        raise HipError("hip route_sigmoid_topk failed")
+
+
 def moe_forward_dev(eset: ExpertSet, x_ptr, S, ids_ptr, w_ptr, k, out_ptr, act_group=0, arm=ARM_AUTO):
     """Async: enqueue one routed MoE layer on the device stream."""
     if lib.coli_hip_moe_forward_dev(eset.ptr, C.c_void_p(x_ptr), S, C.c_void_p(ids_ptr), C.c_void_p(w_ptr), k,

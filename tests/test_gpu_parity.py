@@ -413,3 +413,27 @@ def test_expert_table_many_passes(hip, orc, S, k, E):
     sub = np.arange(0, S, max(1, S // 40))
     ref = orc.moe_forward(x, ids, w, ora, 32, subset=sub, nthreads=8)
     assert np.array_equal(out[sub], ref[sub])
+
+
+@pytest.mark.parametrize("min_share,norm,scale", [(0.0, True, 2.5), (0.05, True, 1.0), (0.02, False, 1.7)])
+def test_sigmoid_router_matches_oracle(hip, orc, min_share, norm, scale):
+    """The reference router (router.rs:52-170) on the device equals the
+    oracle bit-for-bit: bias-augmented selection, ties, NaN and -inf logits,
+    the negligible tail and renormalisation."""
+    say("sigmoid router", min_share, norm, scale)
+    rng = np.random.default_rng(31)
+    S, E, k = 37, 160, 8
+    logits = rng.standard_normal((S, E)).astype(np.float32) * 3
+    logits[0, 5] = logits[0, 9] = 4.0          # ties go to the lower index
+    logits[1, :] = np.nan                      # nothing selectable
+    logits[2, : E - 3] = np.nan                # fewer than k selectable
+    logits[3, 7] = -np.inf
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    bl, bb = hip.DeviceBuffer.from_array(logits), hip.DeviceBuffer.from_array(bias)
+    bids, bw, bk = hip.DeviceBuffer(S * k * 4), hip.DeviceBuffer(S * k * 4), hip.DeviceBuffer(S * 4)
+    hip.route_sigmoid_topk_dev(0, bl.ptr, bb.ptr, S, E, k, bids.ptr, bw.ptr, bk.ptr, norm, scale, min_share)
+    hip.pipe_sync(0)
+    ids, w, keff = orc.route_sigmoid(logits, bias, k, norm, scale, min_share)
+    assert np.array_equal(bids.download(np.int32, (S, k)), ids)
+    assert bw.download(np.float32, (S, k)).tobytes() == w.tobytes()
+    assert np.array_equal(bk.download(np.int32, (S,)), keff)

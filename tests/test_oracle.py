@@ -284,6 +284,34 @@ def test_route_sigmoid_normalises(orc):
         assert sorted(idx[s]) == sorted(top)
 
 
+def test_negligible_tail_reference_cases(orc):
+    """router.rs:531-554: only a trailing run under min_share is dropped, at
+    most kept-1, and degenerate rows are left alone."""
+    w = np.array([0.9, 0.05, 0.03, 0.02], np.float32)
+    assert orc.negligible_tail(w, 4, 0.06) == 3
+    assert orc.negligible_tail(w, 4, 0.04) == 2
+    assert orc.negligible_tail(w, 4, 0.01) == 0
+    assert orc.negligible_tail(np.array([0.5, 0.01, 0.48, 0.01], np.float32), 4, 0.05) == 1
+    assert orc.negligible_tail(np.full(4, 0.25, np.float32), 4, 0.99) == 3
+    assert orc.negligible_tail(np.array([1.0], np.float32), 1, 0.99) == 0
+    assert orc.negligible_tail(np.array([0.0, 0.0], np.float32), 2, 0.5) == 0
+    assert orc.negligible_tail(np.array([np.nan, 1.0], np.float32), 2, 0.5) == 0
+
+
+def test_route_truncates_and_renormalises_to_the_original_scale(orc):
+    """router.rs:557-584: logits 6 and -6 (x = 1 through router weights 6, -6),
+    k = 2, renormalised, routed_scale 2.5: min_share 0.05 drops the negligible
+    expert and the survivor still carries the whole routed_scale."""
+    logits = np.array([[6.0, -6.0]], np.float32)
+    bias = np.zeros(2, np.float32)
+    i_off, w_off, k_off = orc.route_sigmoid(logits, bias, 2, True, 2.5, 0.0)
+    i_on, w_on, k_on = orc.route_sigmoid(logits, bias, 2, True, 2.5, 0.05)
+    assert k_off[0] == 2 and k_on[0] == 1
+    assert i_on[0, 0] == i_off[0, 0] == 0
+    assert abs(float(w_on[0, :1].sum()) - 2.5) < 1e-5 and abs(float(w_off[0, :2].sum()) - 2.5) < 1e-5
+    assert i_on[0, 1] == 0 and w_on[0, 1] == 0.0
+
+
 def test_route_softmax_topk_equals_renormalised_softmax(orc):
     rng = np.random.default_rng(4)
     logits = rng.standard_normal((6, 160)).astype(np.float32)
