@@ -437,3 +437,41 @@ def test_sigmoid_router_matches_oracle(hip, orc, min_share, norm, scale):
     assert np.array_equal(bids.download(np.int32, (S, k)), ids)
     assert bw.download(np.float32, (S, k)).tobytes() == w.tobytes()
     assert np.array_equal(bk.download(np.int32, (S,)), keff)
+
+
+@pytest.mark.parametrize("fmt", [qt.FMT_I4G, qt.FMT_I4, qt.FMT_I8])
+def test_experts_from_qt_container(hip, orc, fmt, tmp_path):
+    """The QT loader bridge: experts written to a model.safetensors container
+    (some tensors kblock-tiled) are detected, read and uploaded; the expert
+    group then equals the oracle on the row-major bytes, bit-for-bit."""
+    from peregrine_amd import qtfile as Q
+    say("qt container", fmt)
+    rng = np.random.default_rng(700 + fmt)
+    D, I, E = 256, 128, 3
+    blobs, ora = [], []
+    for e in range(E):
+        trip = synth.make_expert(rng, D, I, fmt, 32)
+        shp = ((I, D), (I, D), (D, I))
+        ora.append(tuple(orc.Tensor(t[0], t[1], fmt, i, o, 32) for t, (o, i) in zip(trip, shp)))
+        for m, (name, (o, i)) in enumerate(zip(("gate", "up", "down"), shp)):
+            q = np.asarray(trip[m][0], np.uint8).reshape(-1)
+            sc = np.asarray(trip[m][1], np.float32).reshape(-1)
+            row_bytes = q.size // o
+            if fmt == qt.FMT_I4G and (e + m) % 2 == 0:   # every other tensor kblock-tiled by group
+                blobs.append((f"e{e}.{name}", "U8", [o, row_bytes], Q.to_kblock(q, o, 16), ("kblock", 16)))
+            else:
+                blobs.append((f"e{e}.{name}", "U8", [o, row_bytes], q))
+            blobs.append((f"e{e}.{name}.qs", "F32", [sc.size], sc))
+    Q.write_qt(str(tmp_path / "model.safetensors"), blobs)
+    with Q.QtFile(str(tmp_path)) as f:
+        gpu = [Q.upload_expert(0, f, f"e{e}.gate", f"e{e}.up", f"e{e}.down", D, I) for e in range(E)]
+    rows = [2, 5, 1]
+    x = rng.standard_normal((sum(rows), D)).astype(np.float32)
+    hip.set_act_group(0)
+    hip.set_arm(-1)
+    y = hip.expert_group(gpu, rows, x, D)
+    r0 = 0
+    for e, n in enumerate(rows):
+        ref = orc.expert_swiglu(x[r0:r0 + n], *ora[e], 0)
+        assert np.array_equal(y[r0:r0 + n], ref), e
+        r0 += n
