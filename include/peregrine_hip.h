@@ -120,6 +120,12 @@ int coli_hip_set_act_group(int ga);
 int coli_hip_get_act_group(void);
 /* Force an arm for later calls: -1 automatic, COLI_HIP_ARM_GEMV or _MFMA. */
 int coli_hip_set_arm(int arm);
+/* One-token layers with router logits (coli_hip_moe_forward_logits_dev, S = 1,
+ * GEMV arm, at most 256 experts): route and quantise inside the gate/up GEMV
+ * instead of a separate router launch. -1 automatic (when the gate/up grid has
+ * at least 256 workgroups; COLI_HIP_FUSED_ROUTE=0 in the environment turns the
+ * automatic choice off), 0 never, 1 whenever eligible. */
+int coli_hip_set_fused_route(int mode);
 
 /* ---- NEW: device-resident MoE layer (inputs already in HBM) ---- */
 /* A fixed expert table: expert id e -> (gates[e], ups[e], downs[e]). */

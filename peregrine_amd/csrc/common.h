@@ -100,6 +100,9 @@ __device__ __forceinline__ __attribute__((address_space(1))) T *gptr_w(T *p) {
 
 // Phase timestamp for the optional kernel trace (100 MHz constant clock),
 // taken after every outstanding memory operation of the wave has completed.
+#ifdef PHIP_GEMV_TRACE
+void set_misc_trace(long long *p);
+#endif
 __device__ __forceinline__ long long trace_stamp() {
     __builtin_amdgcn_s_waitcnt(0);
     return (long long)__builtin_amdgcn_s_memrealtime();
@@ -207,6 +210,16 @@ void launch_quant_rows(const QuantArgs &a, hipStream_t st);
 void launch_repack(const uint8_t *raw, const float *raw_sc, int fmt, int I, int O, int gs, uint8_t *w, float *sc,
                    const MatGeom &g, hipStream_t st);
 
+// One-token decode: the gate/up GEMV routes the token and quantises its
+// activation row itself (every workgroup redundantly, no grid-wide wait), so
+// the expert weights start streaming without a separate router launch.
+struct RouteArgs {
+    const float *logits; int E; int k;          // logits [E]; greedy top-k, softmax weights
+    int *ids; float *w; ExpertDesc *row_desc;   // [k] outputs, written by workgroup (0, 0)
+    const float *x; int K; int Kp; int mode;    // activation row f32 [K] -> DotArgs.xq / .sx (mode: ACT_*)
+};
+constexpr int ROUTE_MAX_E = 256;   // 4 logits per lane
+
 struct DotArgs {   // shared by the GEMV and MFMA arms
     const ExpertDesc *desc;
     RowPlan plan;
@@ -218,6 +231,7 @@ struct DotArgs {   // shared by the GEMV and MFMA arms
     int act_zero;                                                       // activation row = 0 (one token)
     int n_rows_fixed;                                                   // >= 0: row count known on the host
     long long *trace;                                                   // optional phase timestamps (tests/tuning)
+    RouteArgs route;                                                    // gate/up GEMV: logits != null -> fused router
 };
 // grid_rows / grid_tiles: host-side upper bounds; the kernels read the true
 // counts from plan.counts and idle the excess workgroups.

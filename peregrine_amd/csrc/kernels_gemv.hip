@@ -15,6 +15,7 @@
 #include <cstdlib>
 
 #include "common.h"
+#include "route.h"
 
 namespace phip {
 
@@ -59,6 +60,12 @@ struct DStore<false> {
 constexpr int GEMV_RING = 2;          // rounds of epilogue inputs held in LDS
 constexpr int GEMV_SPIN_LIMIT = 1 << 22;
 
+// dynamic LDS of the ring: [RING][NW*CH][64] f32 factors + the same count of dots
+template <bool W4, int NW, int CH>
+__host__ __device__ constexpr size_t gemv_ring_bytes() {
+    return ((size_t)GEMV_RING * NW * CH * 64 * (4 + (W4 ? 2 : 4)) + 15) / 16 * 16;
+}
+
 __device__ __forceinline__ void spin_until_geq(int *ctr, int target) {
     for (int spin = 0; spin < GEMV_SPIN_LIMIT; ++spin) {
         if (__hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) return;
@@ -76,7 +83,15 @@ __device__ __forceinline__ void spin_until_geq(int *ctr, int target) {
 // order while later rounds stream; a streaming wave waits only when it is
 // RING rounds ahead of the chain. Per-row weight scales only sum integers.
 // All waits are bounded.
-template <bool W4, int EPI, bool GATEUP, int NW, int CH>
+//
+// ROUTE (gate/up, one token): the workgroup first routes the token (wave 0,
+// greedy top-k over the logits) while the other waves copy the expert
+// descriptor table into LDS and quantise the activation row into xq/sx. Every
+// workgroup computes the same bytes, so the shared xq/sx buffers see only
+// identical writes; each workgroup waits for its own stores before its scalar
+// reads of them. Workgroup (0, 0) publishes ids / weights / row descriptors
+// for the down projection and the combine.
+template <bool W4, int EPI, bool GATEUP, int NW, int CH, bool ROUTE>
 __global__ __launch_bounds__((NW + 1) * 64) void gemv_kernel(DotArgs a, MatGeom g, const int8_t *__restrict__ xq,
                                                              const float *__restrict__ sxv) {
     constexpr int BB = W4 ? 16 : 32;
@@ -102,9 +117,109 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemv_kernel(DotArgs a, MatGeom 
     const int nrows = a.n_rows_fixed >= 0 ? a.n_rows_fixed : a.plan.counts[0];
     if (r >= nrows) return;  // uniform: fewer rows than the grid bound
 
-    // the router may have copied this row's descriptor already (one load
-    // instead of row -> expert id -> descriptor)
-    const ExpertDesc *dsc = a.plan.row_desc ? &a.plan.row_desc[r] : &a.desc[a.plan.row_exp[r]];
+    const ExpertDesc *dsc;
+    if constexpr (ROUTE) {
+        static_assert(GATEUP, "the fused router runs in the gate/up GEMV");
+        __shared__ int r_ids[16];
+        __shared__ float r_max[NW + 1];
+        const RouteArgs &ra = a.route;
+        ExpertDesc *tdesc = (ExpertDesc *)((char *)lds_f + gemv_ring_bytes<W4, NW, CH>());
+        // quantising waves: 1..NW except the one that shares wave 0's SIMD
+        constexpr int QSKIP = 4;
+        const int tq = (int)threadIdx.x - 64 - (wave > QSKIP ? 64 : 0), nq = (NW - 1) * 64;
+        float rmax = 0.0f;
+#ifdef PHIP_GEMV_TRACE
+        __shared__ long long r_tdone;
+#endif
+        uint64_t mykey = 0, first = 0;   // wave 0: the selection, kept for the weights
+        int kept = 0;
+        if (wave == 0) {
+#ifdef PHIP_GEMV_TRACE
+            const long long tw = trace_stamp();
+#endif
+            __builtin_amdgcn_s_setprio(3);   // the selection is every wave's critical path: issue it first
+            // a workgroup needs picks 0..r only; the publishing one needs all k
+            const int k_sel = blockIdx.x == 0 && r == 0 ? ra.k : r + 1;
+            route_select<ROUTE_MAX_E / 64>(ra.logits, ra.E, k_sel, mykey, kept, first);
+            __builtin_amdgcn_s_setprio(0);
+            if (lane < k_sel) r_ids[lane] = lane < kept ? route_key_index(mykey) : 0;
+#ifdef PHIP_GEMV_TRACE
+            if (lane == 0) r_tdone = trace_stamp() - tw;
+#endif
+        } else if (wave != QSKIP) {
+            const uint4 *src = (const uint4 *)a.desc;
+            uint4 *dst = (uint4 *)tdesc;
+            const int n16 = ra.E * (int)(sizeof(ExpertDesc) / 16);
+            for (int i = tq; i < n16; i += nq) dst[i] = src[i];
+            const int ngr = ra.Kp >> 3;   // 8-element groups; a 32-block is 4 consecutive lanes
+            const bool vec = (ra.K & 7) == 0 && ((uintptr_t)ra.x & 15) == 0;
+            for (int base = 0; base < ngr; base += nq) {
+                const int gi = base + tq;
+                float v[8];
+                load_group8(ra.x, gi < ngr ? gi : ngr, ra.K, vec, v);   // past the row: zeros
+                float m = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; j++) m = fmaxf(m, fabsf(v[j]));
+                if (ra.mode == ACT_B32) {
+                    m = quad_max(m);
+                    uint2 pk;
+                    const float sc = quant_group8(v, m, pk);
+                    if (gi < ngr) {
+                        *(uint2 *)(const_cast<int8_t *>(a.xq) + (size_t)gi * 8) = pk;
+                        if ((gi & 3) == 0) const_cast<float *>(a.sx)[gi >> 2] = sc;
+                    }
+                } else {
+                    rmax = fmaxf(rmax, m);
+                }
+            }
+            if (ra.mode != ACT_B32) {
+                rmax = warp_max(rmax, 64);
+                if (lane == 0) r_max[wave] = rmax;
+            }
+        }
+        if (ra.mode != ACT_B32) {   // one scale for the row: reduce, then quantise
+            __syncthreads();
+            if (wave != 0 && wave != QSKIP) {
+                float m = 0.0f;
+                for (int w2 = 1; w2 <= NW; w2++)
+                    if (w2 != QSKIP) m = fmaxf(m, r_max[w2]);
+                const int ngr = ra.Kp >> 3;
+                const bool vec = (ra.K & 7) == 0 && ((uintptr_t)ra.x & 15) == 0;
+                for (int gi = tq; gi < ngr; gi += nq) {
+                    float v[8];
+                    load_group8(ra.x, gi, ra.K, vec, v);
+                    uint2 pk;
+                    quant_group8(v, m, pk);
+                    *(uint2 *)(const_cast<int8_t *>(a.xq) + (size_t)gi * 8) = pk;
+                }
+                if (tq == 0) {
+                    float sc = __fdiv_rn(m, 127.0f);
+                    if (sc < 1e-12f) sc = 1e-12f;
+                    const_cast<float *>(a.sx)[0] = sc;
+                }
+            }
+        }
+#ifdef PHIP_GEMV_TRACE
+        long long tq1 = tracing ? trace_stamp() : 0;
+#endif
+        // the quantised row must be in L2 before any wave reads it as scalars
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+#ifdef PHIP_GEMV_TRACE
+        if (tracing && lane == 0) {
+            const long long tb = trace_stamp();
+            a.trace[((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 8 + 7] =
+                ((r_tdone) << 40) | ((tq1 - tr[0]) << 20) | (tb - tr[0]);
+        }
+#endif
+        if (blockIdx.x == 0 && r == 0 && wave == 0)   // one workgroup publishes the routing
+            route_weights(mykey, kept, first, ra.k, ra.ids, ra.w, tdesc, ra.row_desc);
+        dsc = &tdesc[r_ids[r]];
+    } else {
+        // the router may have copied this row's descriptor already (one load
+        // instead of row -> expert id -> descriptor)
+        dsc = a.plan.row_desc ? &a.plan.row_desc[r] : &a.desc[a.plan.row_exp[r]];
+    }
     const int arow = a.act_identity ? r : (a.act_zero ? 0 : a.plan.row_act[r]);
     const int half = lane >> 5, ol = lane & 31;
     const int o = GATEUP ? (int)blockIdx.x * 32 + ol : (int)blockIdx.x * 64 + lane;
@@ -118,8 +233,14 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemv_kernel(DotArgs a, MatGeom 
     // The activation row and its scales are the same for every lane: read
     // them as scalars (constant address space -> scalar loads into SGPRs that
     // v_dot4 takes directly), not through LDS.
-    const CInt *xs = (const CInt *)(uintptr_t)xg;
-    const CFloat *sxs = (const CFloat *)(uintptr_t)sx;
+    uintptr_t xa = (uintptr_t)xg, sa = (uintptr_t)sx;
+    if constexpr (ROUTE) {
+        // the compiler treats constant-space data as invariant: hide the
+        // addresses until after the barrier that follows the quantising stores
+        asm volatile("" : "+s"(xa), "+s"(sa));
+    }
+    const CInt *xs = (const CInt *)xa;
+    const CFloat *sxs = (const CFloat *)sa;
     DT *lds_d = (DT *)(lds_f + (size_t)GEMV_RING * SLOT);
 
     const int nb = g.nb;
@@ -159,7 +280,7 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemv_kernel(DotArgs a, MatGeom 
 #endif
     auto compute_round = [&](int c, const WBlk<W4> (&wv)[CH], const float (&sv)[CH]) {
 #ifdef PHIP_GEMV_TRACE
-        if (a.trace && wave == 0 && c == 1) {
+        if (!ROUTE && a.trace && wave == 0 && c == 1) {
             tw0 = trace_stamp();
             // depend on the first and last weight words: the round's loads have landed
             const int probe = __builtin_amdgcn_readfirstlane((int)(wv[0].a.x ^ wv[CH - 1].a.w));
@@ -199,7 +320,7 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemv_kernel(DotArgs a, MatGeom 
         if (lane == 0)
             __hip_atomic_fetch_add(&produced[c % GEMV_RING], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
 #ifdef PHIP_GEMV_TRACE
-        if (a.trace && wave == 0 && c == 1) {
+        if (!ROUTE && a.trace && wave == 0 && c == 1) {
             tc1 = trace_stamp();
             if (lane == 0) {
                 long long *dst = a.trace + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 8;
@@ -323,12 +444,12 @@ void set_lds_limit(int bytes) { g_lds_limit = bytes > 0 ? bytes : 64 * 1024; }
 
 // gate/up: 7 streaming waves + 1 chain wave (512 threads); down: 3 + 1.
 // Batches of 8 int4 blocks (4 int8 blocks): 4 KB of weights per wave in flight.
-template <bool W4, int EPI, bool GATEUP, int CH>
+template <bool W4, int EPI, bool GATEUP, int CH, bool ROUTE>
 static void launch_gemv_c(const DotArgs &a, const MatGeom &g, int grid_rows, hipStream_t st) {
     constexpr int NW = GATEUP ? 7 : 3;
-    const size_t per_block = 64 * (4 + (W4 ? 2 : 4));
-    const size_t lds = (size_t)GEMV_RING * NW * CH * per_block;
-    auto kern = gemv_kernel<W4, EPI, GATEUP, NW, CH>;
+    // the fused router keeps the expert descriptor table after the ring
+    const size_t lds = gemv_ring_bytes<W4, NW, CH>() + (ROUTE ? (size_t)a.route.E * sizeof(ExpertDesc) : 0);
+    auto kern = gemv_kernel<W4, EPI, GATEUP, NW, CH, ROUTE>;
     static size_t attr_set = 64 * 1024;   // dynamic LDS above 64 KB needs an explicit opt-in
     if (lds > attr_set &&
         hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess)
@@ -341,7 +462,13 @@ static void launch_gemv_c(const DotArgs &a, const MatGeom &g, int grid_rows, hip
 // Batches of 8 int4 blocks (4 int8 blocks): 4 KB of weights per wave per round.
 template <bool W4, int EPI, bool GATEUP>
 static void launch_gemv_t(const DotArgs &a, const MatGeom &g, int grid_rows, hipStream_t st) {
-    launch_gemv_c<W4, EPI, GATEUP, W4 ? 8 : 4>(a, g, grid_rows, st);
+    if constexpr (GATEUP) {
+        if (a.route.logits) {
+            launch_gemv_c<W4, EPI, GATEUP, W4 ? 8 : 4, true>(a, g, grid_rows, st);
+            return;
+        }
+    }
+    launch_gemv_c<W4, EPI, GATEUP, W4 ? 8 : 4, false>(a, g, grid_rows, st);
 }
 
 template <bool GATEUP>

@@ -5,6 +5,7 @@
 #include <algorithm>
 
 #include "common.h"
+#include "route.h"
 
 namespace phip {
 
@@ -157,6 +158,16 @@ __global__ __launch_bounds__(256) void combine_csr_kernel(float *out, const floa
     out[(size_t)s * D + d] = acc;
 }
 
+#ifdef PHIP_GEMV_TRACE
+// debug timeline of the router/quant and combine kernels: [start, mid, end] per workgroup
+__device__ long long *g_misc_trace;
+void set_misc_trace(long long *p) { (void)hipMemcpyToSymbol(HIP_SYMBOL(g_misc_trace), &p, sizeof(p)); }
+#define MISC_STAMP(slot, i) \
+    do { if (g_misc_trace && threadIdx.x == 0) g_misc_trace[(slot) * 4 + (i)] = trace_stamp(); } while (0)
+#else
+#define MISC_STAMP(slot, i) do {} while (0)
+#endif
+
 // Device-table form: token s adds its rows tok_rows[s*k + j] (union order,
 // -1 terminates) weighted by w[s*k + tok_kk[s*k + j]] — the reference scatter
 // out[s] += w * y (mlp.rs:111-119) from a zero row.
@@ -168,6 +179,7 @@ __global__ __launch_bounds__(256) void combine_tok_kernel(float *out, const floa
                                                           const int *tok_kk, const float *w, int k, int D,
                                                           int y_stride, int vec4) {
     const int s = blockIdx.y;
+    MISC_STAMP(1000 + blockIdx.x, 0);
     const int d0 = (blockIdx.x * 256 + threadIdx.x) * 4;
     int rr[16];
     float ww[16];
@@ -200,6 +212,7 @@ __global__ __launch_bounds__(256) void combine_tok_kernel(float *out, const floa
             }
         }
         *(float4 *)(out + (size_t)s * D + d0) = acc;
+        MISC_STAMP(1000 + blockIdx.x, 2);
     } else {
         for (int d = d0; d < min(D, d0 + 4); d++) {
             float acc = 0.0f;
@@ -225,96 +238,6 @@ void launch_combine_tok(float *out, const float *y, const int *tok_rows, const i
 }
 
 // ---------------------------------------------------------------------------
-// Device router for the BASELINE configs: greedy top-k over the logits (strict
-// >, ties to the lowest index — the loop of peregrine-model/src/router.rs:97-118)
-// then w_j = exp(l_j - l_0) / sum_j exp(l_j - l_0) summed in selection order.
-// One wavefront per token.
-// ---------------------------------------------------------------------------
-// (value desc, index asc) maximum across the wavefront, returned uniform.
-// DPP exchanges inside each row of 16 lanes (quad swaps, half-row and row
-// mirrors leave all 16 lanes agreeing), then the four row results are read
-// as scalars.
-template <int CTRL>
-__device__ __forceinline__ void argmax_dpp(float &v, int &i) {
-    const float ov = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-    const int oi = __builtin_amdgcn_update_dpp(0, i, CTRL, 0xF, 0xF, false);
-    if (ov > v || (ov == v && oi < i)) {
-        v = ov;
-        i = oi;
-    }
-}
-__device__ __forceinline__ void wave_argmax(float &v, int &i) {
-    argmax_dpp<0xB1>(v, i);    // quad_perm [1,0,3,2]
-    argmax_dpp<0x4E>(v, i);    // quad_perm [2,3,0,1]
-    argmax_dpp<0x141>(v, i);   // row_half_mirror
-    argmax_dpp<0x140>(v, i);   // row_mirror
-    float bv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    int bi = __builtin_amdgcn_readlane(i, 0);
-#pragma unroll
-    for (int r = 16; r < 64; r += 16) {
-        const float rv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), r));
-        const int ri = __builtin_amdgcn_readlane(i, r);
-        if (rv > bv || (rv == bv && ri < bi)) {
-            bv = rv;
-            bi = ri;
-        }
-    }
-    v = bv;
-    i = bi;
-}
-
-// One wavefront routes one token with the greedy loop itself: k rounds, each
-// picking the largest remaining logit, ties to the lowest index. A lane holds
-// logits e = lane + 64*j; it reduces them in ascending j with a strict `>`,
-// then the wave reduces (value desc, index asc) across lanes. NaN and -inf
-// never qualify (a strict `>` against -inf never picks them), so fewer than k
-// valid logits leave the remaining slots empty, exactly as router.rs:97-118.
-// The winner's owner retires it. desc/row_desc (optional): copy the chosen
-// experts' descriptors per slot.
-template <int PER>
-__device__ void route_token(const float *l, int E, int k, int *ids, float *w, const ExpertDesc *desc,
-                            ExpertDesc *row_desc) {
-    const int lane = threadIdx.x & 63;
-    float ve[PER];
-#pragma unroll
-    for (int j = 0; j < PER; j++) {
-        const int e = lane + 64 * j;
-        const float v = e < E ? l[e] : -INFINITY;
-        ve[j] = v > -INFINITY ? v : -INFINITY;   // NaN, -inf and padding never qualify
-    }
-    float myv = -INFINITY;   // lane kk keeps the kk-th pick
-    int myid = 0, kept = 0;
-    for (int kk = 0; kk < k; kk++) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int j = 0; j < PER; j++)
-            if (ve[j] > bv) {
-                bv = ve[j];
-                bi = lane + 64 * j;
-            }
-        wave_argmax(bv, bi);
-        if (!(bv > -INFINITY)) break;   // uniform: nothing valid remains
-        if (lane == kk) {
-            myv = bv;
-            myid = bi;
-        }
-        if ((bi & 63) == lane) ve[bi >> 6] = -INFINITY;   // retire the pick (PER is small: unrolled select)
-        kept++;
-    }
-    const float l0 = __shfl(myv, 0);
-    const float myex = lane < kept ? exp_cr(__fsub_rn(myv, l0)) : 0.0f;
-    float z = 0.0f;
-    for (int kk = 0; kk < kept; kk++) z = __fadd_rn(z, __shfl(myex, kk));
-    if (lane < k) {
-        const bool ok = lane < kept;
-        const int id = ok ? myid : 0;
-        ids[lane] = id;
-        w[lane] = ok ? __fdiv_rn(myex, z) : 0.0f;
-        if (row_desc) row_desc[lane] = desc[id];
-    }
-}
-
 // The reference's own router (peregrine-model/src/router.rs:52-170, after
 // the router matmul), one wavefront per token: sigmoid scores (exp evaluated
 // as exp_cr), greedy top-k over score + bias with the same argmax rounds,
@@ -433,9 +356,12 @@ __global__ __launch_bounds__(256) void route_quant_kernel(const float *logits, i
                                                           ExpertDesc *row_desc) {
     __shared__ float red[4];
     const int s = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-    if (blockIdx.y == 0 && wave == 0)
+    MISC_STAMP(blockIdx.y, 0);
+    if (blockIdx.y == 0 && wave == 0) {
         route_token<PER>(logits + (size_t)s * E, E, k, ids + (size_t)s * k, w + (size_t)s * k, desc,
                          row_desc ? row_desc + (size_t)s * k : nullptr);
+        MISC_STAMP(blockIdx.y, 1);
+    }
     const float *x = a.x + (size_t)s * a.x_stride;
     int8_t *q = a.q + (size_t)s * a.q_stride;
     if (a.mode == ACT_B32) {
@@ -470,6 +396,7 @@ __global__ __launch_bounds__(256) void route_quant_kernel(const float *logits, i
                 if (sub == 0) a.s[(size_t)s * a.s_stride + b] = sc;
             }
         }
+        MISC_STAMP(blockIdx.y, 2);
     } else {
         constexpr int PX = 32;   // K <= 8192 from registers, the rest re-read
         float v[PX];

@@ -9,6 +9,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -181,6 +182,19 @@ int env_int(const char *name, int dflt) {
 int act_group() {
     if (g_act_group < 0) g_act_group = env_int("COLI_HIP_ACT_GROUP", 0) == 32 ? 32 : 0;
     return g_act_group;
+}
+
+// Fused one-token router: -1 automatic, 0 never, 1 whenever eligible.
+// COLI_HIP_FUSED_ROUTE=0 in the environment turns the automatic choice off.
+std::atomic<int> g_fused_route{-2};
+int fused_route_mode() {
+    int m = g_fused_route.load();
+    if (m == -2) {
+        const char *e = getenv("COLI_HIP_FUSED_ROUTE");
+        m = e && e[0] == '0' ? 0 : -1;
+        g_fused_route.store(m);
+    }
+    return m;
 }
 
 int forced_arm() {
@@ -455,6 +469,7 @@ struct DispatchOpts {
     bool x_quantized = false;   // xq/sx already written (fused router + quant)
     bool act_zero = false;      // every row reads activation row 0 (one token)
     int n_rows_fixed = -1;      // row count known on the host
+    RouteArgs route{};          // one token: router + quant fused into the gate/up GEMV
 };
 
 // The kernel sequence of one dispatch after the activations are on the
@@ -487,6 +502,7 @@ void run_experts(Ctx *c, Prof &prof, const ExpertDesc *desc, const RowPlan &plan
     da.act_identity = x_identity ? 1 : 0;
     da.act_zero = opt.act_zero ? 1 : 0;
     da.n_rows_fixed = opt.n_rows_fixed;
+    da.route = opt.route;
     prof.mark(COLI_HIP_K_GATEUP);
     if (arm == COLI_HIP_ARM_GEMV)
         launch_gemv_gateup(da, gg, act, R_bound, c->stream);
@@ -512,7 +528,11 @@ void run_experts(Ctx *c, Prof &prof, const ExpertDesc *desc, const RowPlan &plan
     dd.trace = g_trace_dn;
     dd.act_identity = 1;
     dd.act_zero = 0;
+    dd.route = RouteArgs{};
     prof.mark(COLI_HIP_K_DOWN);
+#ifdef PHIP_STAGE_EXP
+    if (getenv("PHIP_STAGES") && atoi(getenv("PHIP_STAGES")) < 2) return;
+#endif
     if (arm == COLI_HIP_ARM_GEMV) {
         launch_gemv_down(dd, gd, act, R_bound, c->stream);
     } else {
@@ -931,6 +951,12 @@ int coli_hip_set_arm(int arm) {
     return 1;
 }
 
+int coli_hip_set_fused_route(int mode) {
+    if (mode < -1 || mode > 1) return fail("fused route mode must be -1, 0 or 1");
+    g_fused_route.store(mode);
+    return 1;
+}
+
 int coli_hip_set_profile(int on) {
     g_profile = on ? 1 : 0;
     return 1;
@@ -956,6 +982,9 @@ void coli_hip_reset_stats(void) {
 int coli_hip_set_debug_trace(long long *gateup_dev, long long *down_dev) {
     g_trace_gu = gateup_dev;
     g_trace_dn = down_dev;
+#ifdef PHIP_GEMV_TRACE
+    phip::set_misc_trace(gateup_dev ? gateup_dev + 400000 : nullptr);
+#endif
     return 1;
 }
 
@@ -1090,7 +1119,15 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
         if (!reserve(c, c->rdesc, (size_t)k * sizeof(ExpertDesc))) return 0;
         rdesc = (ExpertDesc *)c->rdesc.p;
     }
-    if (logits_dev) {
+    // fused router: worth it once the gate/up grid covers the chip (the
+    // prologue costs every workgroup ~2 us; with few workgroups the separate
+    // router launch, spread over many, is shorter)
+    const int gu_wgs = k * ((gg.O + 31) / 32), fmode = fused_route_mode();
+    if (logits_dev && one_token && E <= ROUTE_MAX_E && (fmode == 1 || (fmode == -1 && gu_wgs >= 256))) {
+        // the gate/up GEMV routes and quantises the token itself
+        opt.route = RouteArgs{logits_dev, E, k, ids_dev, w_dev, rdesc, x_dev, gg.K, gg.Kp, act};
+        opt.x_quantized = true;
+    } else if (logits_dev) {
         QuantArgs qa{x_dev, gg.K, S, gg.K, gg.Kp, s.xq, s.xs, s.sx, s.sxs, act};
         prof.mark(COLI_HIP_K_QUANT_X);
         launch_route_quant(logits_dev, S, E, k, ids_dev, w_dev, qa, set->desc_dev, rdesc, c->stream);
@@ -1117,6 +1154,9 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
     }
     run_experts(c, prof, set->desc_dev, plan, gg, gd, x_dev, S, false, R, tmax, ga, arm, s, opt);
     prof.mark(COLI_HIP_K_COMBINE);
+#ifdef PHIP_STAGE_EXP
+    if (getenv("PHIP_STAGES") && atoi(getenv("PHIP_STAGES")) < 3) { prof.mark(-1); prof.finish(); return 1; }
+#endif
     if (one_token)   // rows 0..k-1 of token 0, in top-k order
         launch_combine_tok(out_dev, s.y, nullptr, nullptr, w_dev, 1, k, gd.O, s.ys, c->stream);
     else

@@ -344,6 +344,12 @@ def set_arm(arm: int) -> None:
         raise HipError("unknown arm")
 
 
+def set_fused_route(mode: int) -> None:
+    """One-token router inside the gate/up GEMV: -1 automatic, 0 never, 1 whenever eligible."""
+    if lib.coli_hip_set_fused_route(mode) != 1:
+        raise HipError("coli_hip_set_fused_route failed")
+
+
 ARM_AUTO, ARM_MFMA, ARM_GEMV = -1, 0, 2
 
 

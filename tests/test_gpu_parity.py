@@ -222,6 +222,87 @@ def test_router_matches_oracle(hip, orc):
         assert list(idx[0][:2]) == [3, 5]
 
 
+def _adversarial_logits(rng, E):
+    """Rows that stress the greedy selection: many equal values, NaN and
+    -inf (fewer than k valid), +inf, signed zeros, nothing valid."""
+    L = rng.integers(-2, 3, size=(5, E)).astype(np.float32)       # row 0: heavy ties
+    L[1] = -np.inf
+    L[1, rng.choice(E, 5, replace=False)] = rng.standard_normal(5).astype(np.float32)
+    L[1, 0] = np.nan
+    L[2] = 0.0
+    L[2, 1::3] = -0.0
+    L[2, E - 1] = np.inf
+    L[3] = -np.inf                                                   # nothing valid
+    L[4] = rng.standard_normal(E).astype(np.float32)
+    L[4, E // 2] = np.nan
+    return L
+
+
+def test_router_adversarial_matches_oracle(hip, orc):
+    say("router adversarial")
+    rng = np.random.default_rng(81)
+    for E, k in ((200, 8), (64, 8), (256, 16), (9, 4)):
+        logits = _adversarial_logits(rng, E)
+        S = logits.shape[0]
+        bl = hip.DeviceBuffer.from_array(logits)
+        bids, bw = hip.DeviceBuffer(S * k * 4), hip.DeviceBuffer(S * k * 4)
+        hip.route_softmax_topk_dev(0, bl.ptr, S, E, k, bids.ptr, bw.ptr)
+        hip.pipe_sync(0)
+        idx, w = orc.route_softmax_topk(logits, k)
+        assert np.array_equal(bids.download(np.int32, (S, k)), idx), E
+        # +inf as the top logit makes exp(inf - inf) NaN on both sides
+        np.testing.assert_array_equal(bw.download(np.float32, (S, k)), w, err_msg=str(E))
+        assert np.all(idx[3] == 0) and np.all(w[3] == 0)
+
+
+@pytest.mark.parametrize("fused", [1, 0])
+@pytest.mark.parametrize("E,D,I,k,ga", [(200, 320, 192, 8, 32), (256, 100, 64, 6, 0), (5, 264, 96, 3, 32),
+                                         (160, 5120, 1536, 8, 32)])
+def test_one_token_router_paths_match_oracle(hip, orc, fused, E, D, I, k, ga):
+    """One token with router logits: the router inside the gate/up GEMV
+    (fused=1) and the separate router launch (fused=0) both equal the oracle,
+    over normal and adversarial logits, eager and replayed from a graph."""
+    say("one-token router", fused, E, D, I, k, ga)
+    rng = np.random.default_rng(500 + E + D + fused)
+    n_exp = E if D < 1024 else 12
+    gpu, ora = _experts(rng, n_exp, D, I, qt.FMT_I4G, 32, orc, hip)
+    eset = hip.ExpertSet([gpu[e % n_exp] for e in range(E)])
+    ora_full = [ora[e % n_exp] for e in range(E)]
+    cases = [synth.normal_logits(rng, 1, E)] + [row[None, :] for row in _adversarial_logits(rng, E)]
+    bx = hip.DeviceBuffer(D * 4)
+    bl = hip.DeviceBuffer(E * 4)
+    bids, bw, bout = hip.DeviceBuffer(k * 4), hip.DeviceBuffer(k * 4), hip.DeviceBuffer(D * 4)
+    hip.set_fused_route(fused)
+    try:
+        def body():
+            hip.moe_forward_logits_dev(eset, bx.ptr, 1, bl.ptr, k, bids.ptr, bw.ptr, bout.ptr, ga, -1)
+
+        def check(x, logits, tag):
+            ids, w = orc.route_softmax_topk(logits, k)
+            assert np.array_equal(bids.download(np.int32, (1, k)), ids), tag
+            np.testing.assert_array_equal(bw.download(np.float32, (1, k)), w, err_msg=str(tag))   # NaN == NaN
+            ref = orc.moe_forward(x, ids, w, ora_full, ga)
+            got = bout.download(np.float32, (1, D))
+            np.testing.assert_array_equal(got, ref, err_msg=str(tag))
+
+        for ci, logits in enumerate(cases):
+            x = rng.standard_normal((1, D)).astype(np.float32)
+            bx.upload(x)
+            bl.upload(logits)
+            body()
+            hip.pipe_sync(0)
+            check(x, logits, ("eager", ci))
+        g = hip.capture(0, body)
+        for ci, logits in enumerate(cases[:3]):
+            x = rng.standard_normal((1, D)).astype(np.float32)
+            bx.upload(x)
+            bl.upload(logits)
+            g.launch()
+            check(x, logits, ("graph", ci))
+    finally:
+        hip.set_fused_route(-1)
+
+
 @pytest.mark.parametrize("ga", [0, 32])
 @pytest.mark.parametrize("arm", [2, 0])
 def test_moe_layer_matches_oracle(hip, orc, ga, arm):
@@ -245,15 +326,14 @@ def test_moe_layer_matches_oracle(hip, orc, ga, arm):
 @pytest.mark.parametrize("ga", [32, 0])
 def test_moe_layer_fused_router_matches_oracle(hip, orc, S, arm, ga):
     """Router fused with the x quantisation; one token on the GEMV arm runs
-    without an expert table, and the GEMV arm folds the combine into the down
-    projection."""
+    without an expert table."""
     say("fused router layer", S, arm, ga)
     rng = np.random.default_rng(300 + S + arm + ga)
     E, D, I, k = 20, 320, 192, 6
     gpu, ora, eset, x, logits = _layer_case(hip, orc, rng, E, D, I, S, k)
     bx, bl = hip.DeviceBuffer.from_array(x), hip.DeviceBuffer.from_array(logits)
     bids, bw, bout = hip.DeviceBuffer(S * k * 4), hip.DeviceBuffer(S * k * 4), hip.DeviceBuffer(S * D * 4)
-    for rep in range(3):   # repeats: the fused combine's counters reset themselves
+    for rep in range(3):   # repeats: no state may carry over between calls
         hip.moe_forward_logits_dev(eset, bx.ptr, S, bl.ptr, k, bids.ptr, bw.ptr, bout.ptr, ga, arm)
         hip.pipe_sync(0)
         out = bout.download(np.float32, (S, D))
@@ -302,8 +382,7 @@ def test_batched_layer_full_width_sampled(hip, orc):
 @pytest.mark.parametrize("S", [3, 1])
 def test_graph_replay_matches_eager(hip, orc, S):
     """Replays of a captured layer equal eager runs (S = 1 exercises the
-    one-token path, whose down projection also combines through per-tile
-    counters that must rearm between replays)."""
+    one-token path)."""
     say("graph replay", S)
     rng = np.random.default_rng(91 + S)
     E, D, I, k = 8, 256, 128, 2
