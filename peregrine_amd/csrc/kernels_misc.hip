@@ -181,26 +181,27 @@ __global__ __launch_bounds__(256) void combine_tok_kernel(float *out, const floa
     const int s = blockIdx.y;
     MISC_STAMP(1000 + blockIdx.x, 0);
     const int d0 = (blockIdx.x * 256 + threadIdx.x) * 4;
-    int rr[16];
-    float ww[16];
-    int n = 0;
+    // The token's row list and weights: every index load is issued before
+    // any is used (clamped, unconditional), then every weight load.
+    int rr[16], kq[16];
 #pragma unroll
     for (int j = 0; j < 16; j++) {
-        if (j < k && n == j) {
-            const int r = tok_rows ? tok_rows[(size_t)s * k + j] : j;
-            if (r >= 0) {
-                rr[j] = r;
-                ww[j] = w[(size_t)s * k + (tok_kk ? tok_kk[(size_t)s * k + j] : j)];
-                n = j + 1;
-            }
-        }
+        const int jj = min(j, k - 1);
+        rr[j] = tok_rows ? tok_rows[(size_t)s * k + jj] : jj;
+        kq[j] = tok_kk ? tok_kk[(size_t)s * k + jj] : jj;
     }
+    int n = 0;   // rows up to the first -1
+#pragma unroll
+    for (int j = 0; j < 16; j++) n += (j < k && n == j && rr[j] >= 0) ? 1 : 0;
+    float ww[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) ww[j] = w[(size_t)s * k + (j < n ? kq[j] : 0)];
     if (d0 >= D) return;
     if (vec4) {   // D and the row strides are multiples of 4
         float4 yv[16];
 #pragma unroll
-        for (int j = 0; j < 16; j++)
-            if (j < n) yv[j] = *(const float4 *)(y + (size_t)rr[j] * y_stride + d0);
+        for (int j = 0; j < 16; j++)   // past n: row 0, read and ignored (no waits between loads)
+            if (j < k) yv[j] = *(const float4 *)(y + (size_t)(j < n ? rr[j] : 0) * y_stride + d0);
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int j = 0; j < 16; j++) {
