@@ -17,6 +17,8 @@
 //
 // int4 weights are unpacked in registers: 8 bytes (16 nibbles) per lane per
 // block -> 16 int8 values scaled by 16 (the scale tables carry the 1/16).
+#include <cstdlib>
+
 #include "common.h"
 
 namespace phip {
@@ -259,6 +261,258 @@ __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const i
     }
 }
 
+// ---------------------------------------------------------------------------
+// LDS-staged variant for weight-streaming shapes. Each wave copies its own
+// operands of a block (activations, weights, weight scales and, with 32-block
+// activation scales, those too) straight from HBM into a private LDS stage
+// with the LDS-DMA loads, PD blocks ahead, so the bytes in flight no longer
+// cost registers. A wave reads only what it copied itself: no barrier, just a
+// wait for its own older copies. The copies are issued from inline assembly
+// (the compiler would otherwise wait for every copy before any LDS read); the
+// loop issues no other vector-memory operation, so "older than the last
+// OPS*PD" is exactly the block about to be used.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void lds_dma16(const void *g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory");
+}
+__device__ __forceinline__ void lds_dma16_nt(const void *g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(g), "s"(lds) : "memory");
+}
+__device__ __forceinline__ void lds_dma4(const void *g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <bool W4, int EPI>
+struct DmaStage {
+    static constexpr int A = 0;                           // [64 lanes][16 B] activations
+    static constexpr int B = 1024;                        // weights: W4 [2 subtiles][32 cols][16 B], W8 [2][32][32 B]
+    static constexpr int SW = B + (W4 ? 1024 : 2048);     // [2][32] weight scales
+    static constexpr int SX = SW + 256;                   // [32 rows] activation scales (EPI_B32), lanes 32-63 repeat
+    static constexpr int BYTES = SX + (EPI == EPI_B32 ? 256 : 0);
+    static constexpr int OPS = 1 + (W4 ? 1 : 2) + (EPI != EPI_ROW ? 1 : 0) + (EPI == EPI_B32 ? 1 : 0);
+};
+
+template <bool W4, int EPI, bool GATEUP, int NSUB, int PD>
+__global__ __launch_bounds__(256) void mfma_dma_kernel(DotArgs a, MatGeom g) {
+    static_assert(NSUB == 2, "a wave's weight copy covers two 32-column subtiles");
+    typedef DmaStage<W4, EPI> ST;
+    constexpr int NSTG = PD + 2;   // stage b-2 is refilled once block b-2's epilogue has read it
+    constexpr int BB = W4 ? 16 : 32;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds_u8[];   // [4 waves][NSTG][ST::BYTES]
+
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int tile = blockIdx.y;
+    if (tile >= a.plan.counts[1]) return;
+    const int e = a.plan.mt_exp[tile], r0 = a.plan.mt_row0[tile], rend = a.plan.mt_rend[tile];
+    const int j = lane & 31, hh = lane >> 5;
+    const int n0 = GATEUP ? ((int)blockIdx.x * 4 + wave) * 32 : ((int)blockIdx.x * 4 + wave) * 32 * NSUB;
+    uint8_t *wl = lds_u8 + (size_t)wave * NSTG * ST::BYTES;
+    const uint32_t wl_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)wl);
+
+    // copy sources of this lane
+    int ra = r0 + j;   // rows past the expert's end repeat its last row (never stored)
+    if (ra >= rend) ra = rend - 1;
+    const int arow = a.act_identity ? ra : a.plan.row_act[ra];
+    const uint8_t *src_a = (const uint8_t *)a.xq + (size_t)arow * a.x_stride + hh * 16;   // A: lane (j, hh)
+    const float *src_x = a.sx + (size_t)arow * a.sx_stride;                          // SX: lane (j, *)
+    const int sl = lane >> 5;                                                        // copy lane's subtile
+    int oc_l = GATEUP ? n0 + j : n0 + sl * 32 + j;
+    if (oc_l >= g.Op) oc_l = g.Op - 1;
+    const int mat_l = GATEUP ? sl : 2;
+    const uint8_t *src_w;   // W4: lane (subtile sl, col j), 16 B; W8: per op q, lane -> (col l/2, half l%2)
+    if constexpr (W4) {
+        src_w = a.desc[e].w[mat_l] + ((size_t)(oc_l / TILE_O) * g.nb * TILE_O + (oc_l % TILE_O)) * BB;
+    } else {
+        src_w = nullptr;
+    }
+    const float *src_s = a.desc[e].sc[mat_l] + (size_t)(oc_l / TILE_O) * g.ng * TILE_O + (oc_l % TILE_O);
+    const uint8_t *src_w8[2] = {nullptr, nullptr};
+    if constexpr (!W4) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            int o = GATEUP ? n0 + (lane >> 1) : n0 + q * 32 + (lane >> 1);
+            if (o >= g.Op) o = g.Op - 1;
+            const int mat = GATEUP ? q : 2;
+            src_w8[q] = a.desc[e].w[mat] + ((size_t)(o / TILE_O) * g.nb * TILE_O + (o % TILE_O)) * BB + (lane & 1) * 16;
+        }
+    }
+    auto copy_blk = [&](int b) {
+        const int bc = b < g.nb ? b : g.nb - 1;
+        const uint32_t st = wl_addr + (uint32_t)((b % NSTG) * ST::BYTES);
+        lds_dma16(src_a + (size_t)bc * BLK, st + ST::A);
+        if constexpr (W4) {
+            lds_dma16_nt(src_w + (size_t)bc * TILE_O * BB, st + ST::B);
+        } else {
+            lds_dma16_nt(src_w8[0] + (size_t)bc * TILE_O * BB, st + ST::B);
+            lds_dma16_nt(src_w8[1] + (size_t)bc * TILE_O * BB, st + ST::B + 1024);
+        }
+        if constexpr (EPI != EPI_ROW) lds_dma4(src_s + (size_t)grp_of(bc, g.gshift) * TILE_O, st + ST::SW);
+        if constexpr (EPI == EPI_B32) lds_dma4(src_x + bc, st + ST::SX);
+    };
+
+    int oc[NSUB];
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) oc[s] = GATEUP ? n0 + j : n0 + s * 32 + j;
+    float acc[NSUB][16];
+    v16i iacc[NSUB];
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[s][i] = 0.0f;
+        iacc[s] = v16i{};
+    }
+    const int nrow = rend - r0;
+
+    auto read_ops = [&](int b, v4i &A, v4i (&B)[NSUB], float (&S)[NSUB]) {
+        const uint8_t *st = wl + (b % NSTG) * ST::BYTES;
+        A = *(const v4i *)(st + ST::A + lane * 16);
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) {
+            if constexpr (W4) {
+                const uint2 w = *(const uint2 *)(st + ST::B + (s * 32 + j) * 16 + hh * 8);
+                B[s][0] = i4_even16(w.x);
+                B[s][1] = i4_odd16(w.x);
+                B[s][2] = i4_even16(w.y);
+                B[s][3] = i4_odd16(w.y);
+            } else {
+                B[s] = *(const v4i *)(st + ST::B + s * 1024 + j * 32 + hh * 16);
+            }
+            if constexpr (EPI != EPI_ROW) S[s] = *(const float *)(st + ST::SW + (s * 32 + j) * 4);
+        }
+    };
+    auto mma_blk = [&](int b, const v4i &A, const v4i (&B)[NSUB], v16i (&D)[NSUB]) {
+        const bool opens = EPI == EPI_B32 || (EPI == EPI_GRP && (b == 0 || grp_end(b - 1, g.gshift, g.nb))) ||
+                           (EPI == EPI_ROW && b == 0);
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) {
+            const v16i cin = opens ? v16i{} : iacc[s];
+            D[s] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B[s], cin, 0, 0, 0);
+            if (EPI != EPI_B32) iacc[s] = D[s];
+        }
+    };
+    auto epi_blk = [&](int b, const v16i (&D)[NSUB], const float (&S)[NSUB]) {
+        if constexpr (EPI == EPI_ROW) return;
+        if (EPI == EPI_GRP && !grp_end(b, g.gshift, g.nb)) return;
+        if constexpr (EPI == EPI_B32) {
+            const float4 *sx4 = (const float4 *)(wl + (b % NSTG) * ST::BYTES + ST::SX + 16 * hh);
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+                if (8 * gq >= nrow) break;   // uniform: rows past the tile's end
+                const float4 sq = sx4[2 * gq];
+                const float sxr[4] = {sq.x, sq.y, sq.z, sq.w};
+#pragma unroll
+                for (int s = 0; s < NSUB; ++s) {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const int i = 4 * gq + t;
+                        acc[s][i] = __fmaf_rn(__fmul_rn(S[s], sxr[t]), (float)D[s][i], acc[s][i]);
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+                if (8 * gq >= nrow) break;
+#pragma unroll
+                for (int s = 0; s < NSUB; ++s) {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const int i = 4 * gq + t;
+                        acc[s][i] = __fadd_rn(acc[s][i], __fmul_rn((float)D[s][i], S[s]));
+                    }
+                }
+            }
+        }
+    };
+
+#pragma unroll
+    for (int u = 0; u < PD; ++u) copy_blk(u);
+    v16i Dr[2][NSUB];
+    float Sr[2][NSUB];
+#pragma unroll 1
+    for (int b = 0; b < g.nb; b += 2) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int bb = b + u;
+            if (bb < g.nb) {   // uniform
+                copy_blk(bb + PD);
+                wait_vm<ST::OPS * PD>();   // block bb's copies have landed
+                v4i A;
+                v4i B[NSUB];
+                read_ops(bb, A, B, Sr[u]);
+                mma_blk(bb, A, B, Dr[u]);
+            }
+            if (bb > 0 && bb - 1 < g.nb) epi_blk(bb - 1, Dr[u ^ 1], Sr[u ^ 1]);
+        }
+    }
+    if (g.nb % 2 == 0) epi_blk(g.nb - 1, Dr[1], Sr[1]);   // the last block's epilogue did not run in the loop
+    wait_vm<0>();   // the clamped copies past the end land before the workgroup can exit
+
+    // per-row activation scale (EPI_ROW / EPI_GRP) of each accumulator row
+    float v[NSUB][16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        float sxr = 1.0f;
+        if constexpr (EPI != EPI_B32) {
+            int rr = r0 + acc_row(i, lane);
+            if (rr >= rend) rr = rend - 1;
+            const int ar = a.act_identity ? rr : a.plan.row_act[rr];
+            sxr = a.sx[(size_t)ar * a.sx_stride];
+        }
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) {
+            if constexpr (EPI == EPI_ROW) {
+                const int D = W4 ? (iacc[s][i] >> 4) : iacc[s][i];
+                int o = oc[s];
+                if (o >= g.Op) o = g.Op - 1;
+                const int mat = GATEUP ? s : 2;
+                const float *sp = a.desc[e].sc[mat] + (size_t)(o / TILE_O) * g.ng * TILE_O + (o % TILE_O);
+                const float sc = W4 ? __fmul_rn(sp[0], 16.0f) : sp[0];
+                v[s][i] = __fmul_rn(__fmul_rn((float)D, sc), sxr);
+            } else if constexpr (EPI == EPI_GRP) {
+                v[s][i] = __fmul_rn(acc[s][i], sxr);
+            } else {
+                v[s][i] = acc[s][i];
+            }
+        }
+    }
+
+    if constexpr (GATEUP) {
+        const int o = oc[0];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int row = r0 + acc_row(i, lane);
+            const float h = silu_mul(v[0][i], v[1][i]);
+            const bool ok = row < rend && o < ((g.O + 31) & ~31);
+            if (ok) a.out[(size_t)row * a.out_stride + o] = h;
+            if (EPI == EPI_B32 && a.hq) {
+                const float m = warp_max(fabsf(h), 32);
+                float sc = __fdiv_rn(m, 127.0f);
+                if (sc < 1e-12f) sc = 1e-12f;
+                const float inv = __fdiv_rn(1.0f, sc);
+                if (ok) {
+                    a.hq[(size_t)row * a.hq_stride + perm8(o)] = (int8_t)(int)rintf(__fmul_rn(h, inv));
+                    if (j == 0) a.sh[(size_t)row * a.sh_stride + (o >> 5)] = sc;
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) {
+            const int o = oc[s];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int row = r0 + acc_row(i, lane);
+                if (row < rend && o < g.O) a.out[(size_t)row * a.out_stride + o] = v[s][i];
+            }
+        }
+    }
+}
+
 template <bool W4, int EPI, bool GATEUP, int PD>
 static void launch_mfma_p(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
     constexpr int NSUB = 2;
@@ -269,8 +523,39 @@ static void launch_mfma_p(const DotArgs &a, const MatGeom &g, int grid_tiles, hi
     hipLaunchKernelGGL((mfma_kernel<W4, EPI, GATEUP, NSUB, PD>), grid, dim3(256), lds, st, a, g, a.xq, a.sx);
 }
 
+template <bool W4, int EPI, bool GATEUP, int PD>
+static void launch_mfma_dma(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
+    constexpr int NSUB = 2;
+    const int ch_per_wg = GATEUP ? 4 * 32 : 4 * 32 * NSUB;
+    const int span = GATEUP ? ((g.O + 31) & ~31) : g.O;
+    dim3 grid((unsigned)((span + ch_per_wg - 1) / ch_per_wg), (unsigned)grid_tiles);
+    const size_t lds = (size_t)4 * (PD + 2) * DmaStage<W4, EPI>::BYTES;
+    auto kern = mfma_dma_kernel<W4, EPI, GATEUP, NSUB, PD>;
+    static size_t attr_set = 64 * 1024;
+    if (lds > attr_set &&
+        hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess)
+        attr_set = lds;
+    hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, a, g);
+}
+
+// COLI_HIP_MFMA_DMA: -1 (default) LDS-staged for weight-streaming int4
+// dispatches (few rows per expert), register prefetch otherwise; 0 / 1 force
+// one kernel (A/B measurement).
+static int mfma_mode() {
+    static const int m = getenv("COLI_HIP_MFMA_DMA") ? atoi(getenv("COLI_HIP_MFMA_DMA")) : -1;
+    return m;
+}
+
 template <bool W4, int EPI, bool GATEUP>
 static void launch_mfma_t(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
+    const int m = mfma_mode();
+    // int8 weights carry twice the bytes per MFMA: the register-prefetch
+    // kernel already streams them near its limit, and their larger stages
+    // leave the staged kernel a shallower pipeline (measured slower)
+    if (!a.dots && (m == 1 || (m < 0 && W4 && a.mfma_stream))) {
+        launch_mfma_dma<W4, EPI, GATEUP, W4 ? 5 : 3>(a, g, grid_tiles, st);
+        return;
+    }
     launch_mfma_p<W4, EPI, GATEUP, 2>(a, g, grid_tiles, st);   // two blocks ahead: deeper costs occupancy
 }
 

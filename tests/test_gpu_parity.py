@@ -344,6 +344,21 @@ def test_moe_layer_fused_router_matches_oracle(hip, orc, S, arm, ga):
         assert np.array_equal(out, ref), (rep, nerr(out, ref))
 
 
+@pytest.mark.parametrize("ga", [32, 0])
+@pytest.mark.parametrize("fmt,gs", FORMATS)
+def test_mfma_dense_and_streaming_dispatches(hip, orc, ga, fmt, gs):
+    """The MFMA arm picks its LDS-staged kernel when experts get fewer rows
+    than one 32-row tile on average and the register-prefetch kernel when they
+    get more: both dispatches equal the oracle bit for bit."""
+    say("mfma dense/streaming", ga, fmt, gs)
+    rng = np.random.default_rng(610 + ga + fmt)
+    for E, S, k in ((3, 64, 2), (16, 9, 3)):   # 43 rows per expert, then under 2
+        gpu, ora, eset, x, logits = _layer_case(hip, orc, rng, E, 288, 160, S, k, fmt=fmt, gs=gs or 32)
+        out, ids, w = _run_layer(hip, eset, x, logits, k, ga, 2)
+        ref = orc.moe_forward(x, ids, w, ora, ga)
+        assert np.array_equal(out, ref), (E, S, k, nerr(out, ref))
+
+
 def test_moe_layer_arms_agree_and_repeat(hip, orc):
     say("arms agree")
     rng = np.random.default_rng(77)
