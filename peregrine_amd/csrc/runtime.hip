@@ -920,7 +920,10 @@ int coli_hip_pipe_download(int device, const void *src, void *dst, size_t bytes)
 int coli_hip_event_record(int device, int slot) {
     Ctx *c = find_ctx(device);
     if (slot < 0 || slot >= 16 || !select_ctx(c)) return 0;
-    if (!c->user_ev[slot] && !hip_ok(hipEventCreate(&c->user_ev[slot]), "event create")) return 0;
+    // device-stream timing only: no system-scope fence (as the profiler's events)
+    if (!c->user_ev[slot] &&
+        !hip_ok(hipEventCreateWithFlags(&c->user_ev[slot], hipEventDisableSystemFence), "event create"))
+        return 0;
     return hip_ok(hipEventRecord(c->user_ev[slot], c->stream), "event record");
 }
 
