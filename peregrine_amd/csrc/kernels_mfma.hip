@@ -47,6 +47,24 @@ __device__ __forceinline__ v4i load_b(GU8 *p) {
 
 __device__ __forceinline__ int acc_row(int reg, int lane) { return 8 * (reg >> 2) + 4 * (lane >> 5) + (reg & 3); }
 
+// The per-32 activation scales of a tile's 32 rows into LDS, [nb][32]: eight
+// threads per row read consecutive blocks, four loads in flight per thread
+// (rows past the expert's end repeat its last row).
+__device__ __forceinline__ void load_tile_sx(const DotArgs &a, int r0, int rend, int nb, float *sxl) {
+    const int i = threadIdx.x >> 3, b0 = threadIdx.x & 7;
+    int rr = r0 + i;
+    if (rr >= rend) rr = rend - 1;
+    const float *src = a.sx + (size_t)(a.act_identity ? rr : a.plan.row_act[rr]) * a.sx_stride;
+    for (int bb = b0; bb < nb; bb += 32) {
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = bb + 8 * q < nb ? src[bb + 8 * q] : 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (bb + 8 * q < nb) sxl[(bb + 8 * q) * 32 + i] = v[q];
+    }
+}
+
 // NSUB column subtiles of 32 per wave. GATEUP: subtile 0 = gate, 1 = up (same
 // channels). Down: NSUB adjacent 32-channel subtiles.
 template <bool W4, int EPI, bool GATEUP, int NSUB, int PD>
@@ -70,13 +88,7 @@ __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const i
     GU8 *xa = (GU8 *)gptr(xq + (size_t)arow_a * a.x_stride + hh * 16);
 
     if constexpr (EPI == EPI_B32) {
-        for (int idx = threadIdx.x; idx < 32 * g.nb; idx += 256) {
-            const int i = idx & 31, b = idx >> 5;
-            int rr = r0 + i;
-            if (rr >= rend) rr = rend - 1;
-            const int ar = a.act_identity ? rr : a.plan.row_act[rr];
-            sxl[b * 32 + i] = sxv[(size_t)ar * a.sx_stride + b];
-        }
+        load_tile_sx(a, r0, rend, g.nb, sxl);
         __syncthreads();
     }
 
@@ -286,23 +298,30 @@ __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <bool W4, int EPI>
+// One stage (a block in flight), shared by the workgroup's four waves:
+// [A: 32 activation rows x 32 B] then, per wave, [weights of its two
+// subtiles][their scales]. Each wave copies a quarter of A (8 rows) and its
+// own weights and scales: the same copy count for every wave, so one constant
+// wait count holds, and one barrier per block makes the quarters of A visible
+// to all. Per-32 activation scales for the whole tile sit after the stages,
+// loaded once.
+template <bool W4>
 struct DmaStage {
-    static constexpr int A = 0;                           // [64 lanes][16 B] activations
-    static constexpr int B = 1024;                        // weights: W4 [2 subtiles][32 cols][16 B], W8 [2][32][32 B]
-    static constexpr int SW = B + (W4 ? 1024 : 2048);     // [2][32] weight scales
-    static constexpr int SX = SW + 256;                   // [32 rows] activation scales (EPI_B32), lanes 32-63 repeat
-    static constexpr int BYTES = SX + (EPI == EPI_B32 ? 256 : 0);
-    static constexpr int OPS = 1 + (W4 ? 1 : 2) + (EPI != EPI_ROW ? 1 : 0) + (EPI == EPI_B32 ? 1 : 0);
+    static constexpr int A = 0;
+    static constexpr int WAVE0 = 1024;
+    static constexpr int SW = W4 ? 1024 : 2048;   // within a wave's part: weights, then scales
+    static constexpr int WAVE_BYTES = SW + 256;
+    static constexpr int BYTES = WAVE0 + 4 * WAVE_BYTES;
 };
 
 template <bool W4, int EPI, bool GATEUP, int NSUB, int PD>
 __global__ __launch_bounds__(256) void mfma_dma_kernel(DotArgs a, MatGeom g) {
     static_assert(NSUB == 2, "a wave's weight copy covers two 32-column subtiles");
-    typedef DmaStage<W4, EPI> ST;
-    constexpr int NSTG = PD + 2;   // stage b-2 is refilled once block b-2's epilogue has read it
+    typedef DmaStage<W4> ST;
+    constexpr int NSTG = PD + 2;   // stage b-2 is refilled once every wave is past block b-1's barrier
+    constexpr int OPS = 1 + (W4 ? 1 : 2) + (EPI != EPI_ROW ? 1 : 0);   // copies per block and wave
     constexpr int BB = W4 ? 16 : 32;
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds_u8[];   // [4 waves][NSTG][ST::BYTES]
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds_u8[];   // [NSTG][ST::BYTES], then sxl
 
     const int lane = threadIdx.x & 63, wave = wave_id();
     const int tile = blockIdx.y;
@@ -310,25 +329,22 @@ __global__ __launch_bounds__(256) void mfma_dma_kernel(DotArgs a, MatGeom g) {
     const int e = a.plan.mt_exp[tile], r0 = a.plan.mt_row0[tile], rend = a.plan.mt_rend[tile];
     const int j = lane & 31, hh = lane >> 5;
     const int n0 = GATEUP ? ((int)blockIdx.x * 4 + wave) * 32 : ((int)blockIdx.x * 4 + wave) * 32 * NSUB;
-    uint8_t *wl = lds_u8 + (size_t)wave * NSTG * ST::BYTES;
-    const uint32_t wl_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)wl);
+    const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_u8);
+    float *sxl = (float *)(lds_u8 + (size_t)NSTG * ST::BYTES);   // EPI_B32: [nb][32] activation scales
 
-    // copy sources of this lane
-    int ra = r0 + j;   // rows past the expert's end repeat its last row (never stored)
+    // copy sources of this lane: a dword of A (row 8*wave + lane/8), its
+    // weights (subtile lane/32, column lane%32) and their scales; rows past
+    // the expert's end repeat its last row (never stored)
+    int ra = r0 + 8 * wave + (lane >> 3);
     if (ra >= rend) ra = rend - 1;
-    const int arow = a.act_identity ? ra : a.plan.row_act[ra];
-    const uint8_t *src_a = (const uint8_t *)a.xq + (size_t)arow * a.x_stride + hh * 16;   // A: lane (j, hh)
-    const float *src_x = a.sx + (size_t)arow * a.sx_stride;                          // SX: lane (j, *)
-    const int sl = lane >> 5;                                                        // copy lane's subtile
+    const uint8_t *src_a = (const uint8_t *)a.xq +
+                           (size_t)(a.act_identity ? ra : a.plan.row_act[ra]) * a.x_stride + (lane & 7) * 4;
+    const int sl = lane >> 5;
     int oc_l = GATEUP ? n0 + j : n0 + sl * 32 + j;
     if (oc_l >= g.Op) oc_l = g.Op - 1;
     const int mat_l = GATEUP ? sl : 2;
-    const uint8_t *src_w;   // W4: lane (subtile sl, col j), 16 B; W8: per op q, lane -> (col l/2, half l%2)
-    if constexpr (W4) {
-        src_w = a.desc[e].w[mat_l] + ((size_t)(oc_l / TILE_O) * g.nb * TILE_O + (oc_l % TILE_O)) * BB;
-    } else {
-        src_w = nullptr;
-    }
+    const uint8_t *src_w = nullptr;
+    if constexpr (W4) src_w = a.desc[e].w[mat_l] + ((size_t)(oc_l / TILE_O) * g.nb * TILE_O + (oc_l % TILE_O)) * BB;
     const float *src_s = a.desc[e].sc[mat_l] + (size_t)(oc_l / TILE_O) * g.ng * TILE_O + (oc_l % TILE_O);
     const uint8_t *src_w8[2] = {nullptr, nullptr};
     if constexpr (!W4) {
@@ -342,17 +358,24 @@ __global__ __launch_bounds__(256) void mfma_dma_kernel(DotArgs a, MatGeom g) {
     }
     auto copy_blk = [&](int b) {
         const int bc = b < g.nb ? b : g.nb - 1;
-        const uint32_t st = wl_addr + (uint32_t)((b % NSTG) * ST::BYTES);
-        lds_dma16(src_a + (size_t)bc * BLK, st + ST::A);
+        const uint32_t st = lds_addr + (uint32_t)((b % NSTG) * ST::BYTES);
+        const uint32_t wv = st + ST::WAVE0 + wave * ST::WAVE_BYTES;
+        lds_dma4(src_a + (size_t)bc * BLK, st + ST::A + wave * 256);
         if constexpr (W4) {
-            lds_dma16_nt(src_w + (size_t)bc * TILE_O * BB, st + ST::B);
+            lds_dma16_nt(src_w + (size_t)bc * TILE_O * BB, wv);
         } else {
-            lds_dma16_nt(src_w8[0] + (size_t)bc * TILE_O * BB, st + ST::B);
-            lds_dma16_nt(src_w8[1] + (size_t)bc * TILE_O * BB, st + ST::B + 1024);
+            lds_dma16_nt(src_w8[0] + (size_t)bc * TILE_O * BB, wv);
+            lds_dma16_nt(src_w8[1] + (size_t)bc * TILE_O * BB, wv + 1024);
         }
-        if constexpr (EPI != EPI_ROW) lds_dma4(src_s + (size_t)grp_of(bc, g.gshift) * TILE_O, st + ST::SW);
-        if constexpr (EPI == EPI_B32) lds_dma4(src_x + bc, st + ST::SX);
+        if constexpr (EPI != EPI_ROW) lds_dma4(src_s + (size_t)grp_of(bc, g.gshift) * TILE_O, wv + ST::SW);
     };
+
+    // the tile's activation scales first (the compiler waits for these
+    // loads, and a wave's loads complete in order), then the first copies
+    if constexpr (EPI == EPI_B32) load_tile_sx(a, r0, rend, g.nb, sxl);
+#pragma unroll
+    for (int u = 0; u < PD; ++u)
+        if (u < g.nb) copy_blk(u);
 
     int oc[NSUB];
 #pragma unroll
@@ -368,20 +391,21 @@ __global__ __launch_bounds__(256) void mfma_dma_kernel(DotArgs a, MatGeom g) {
     const int nrow = rend - r0;
 
     auto read_ops = [&](int b, v4i &A, v4i (&B)[NSUB], float (&S)[NSUB]) {
-        const uint8_t *st = wl + (b % NSTG) * ST::BYTES;
-        A = *(const v4i *)(st + ST::A + lane * 16);
+        const uint8_t *st = lds_u8 + (b % NSTG) * ST::BYTES;
+        const uint8_t *wv = st + ST::WAVE0 + wave * ST::WAVE_BYTES;
+        A = *(const v4i *)(st + ST::A + j * 32 + hh * 16);
 #pragma unroll
         for (int s = 0; s < NSUB; ++s) {
             if constexpr (W4) {
-                const uint2 w = *(const uint2 *)(st + ST::B + (s * 32 + j) * 16 + hh * 8);
+                const uint2 w = *(const uint2 *)(wv + (s * 32 + j) * 16 + hh * 8);
                 B[s][0] = i4_even16(w.x);
                 B[s][1] = i4_odd16(w.x);
                 B[s][2] = i4_even16(w.y);
                 B[s][3] = i4_odd16(w.y);
             } else {
-                B[s] = *(const v4i *)(st + ST::B + s * 1024 + j * 32 + hh * 16);
+                B[s] = *(const v4i *)(wv + s * 1024 + j * 32 + hh * 16);
             }
-            if constexpr (EPI != EPI_ROW) S[s] = *(const float *)(st + ST::SW + (s * 32 + j) * 4);
+            if constexpr (EPI != EPI_ROW) S[s] = *(const float *)(wv + ST::SW + (s * 32 + j) * 4);
         }
     };
     auto mma_blk = [&](int b, const v4i &A, const v4i (&B)[NSUB], v16i (&D)[NSUB]) {
@@ -398,7 +422,7 @@ __global__ __launch_bounds__(256) void mfma_dma_kernel(DotArgs a, MatGeom g) {
         if constexpr (EPI == EPI_ROW) return;
         if (EPI == EPI_GRP && !grp_end(b, g.gshift, g.nb)) return;
         if constexpr (EPI == EPI_B32) {
-            const float4 *sx4 = (const float4 *)(wl + (b % NSTG) * ST::BYTES + ST::SX + 16 * hh);
+            const float4 *sx4 = (const float4 *)(sxl + b * 32 + 4 * hh);
 #pragma unroll
             for (int gq = 0; gq < 4; ++gq) {
                 if (8 * gq >= nrow) break;   // uniform: rows past the tile's end
@@ -429,8 +453,6 @@ __global__ __launch_bounds__(256) void mfma_dma_kernel(DotArgs a, MatGeom g) {
         }
     };
 
-#pragma unroll
-    for (int u = 0; u < PD; ++u) copy_blk(u);
     v16i Dr[2][NSUB];
     float Sr[2][NSUB];
 #pragma unroll 1
@@ -439,8 +461,16 @@ __global__ __launch_bounds__(256) void mfma_dma_kernel(DotArgs a, MatGeom g) {
         for (int u = 0; u < 2; ++u) {
             const int bb = b + u;
             if (bb < g.nb) {   // uniform
-                copy_blk(bb + PD);
-                wait_vm<ST::OPS * PD>();   // block bb's copies have landed
+                if (bb + PD < g.nb) {
+                    copy_blk(bb + PD);
+                    wait_vm<OPS * PD>();   // this wave's copies of block bb have landed
+                } else {
+                    wait_vm<0>();          // the last blocks: nothing copied past the end
+                }
+                // every wave's quarter of A (and, on the first pass, the
+                // activation scales) is in LDS once all waves are here
+                if (bb == 0) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // + sxl
+                else asm volatile("s_barrier" ::: "memory");
                 v4i A;
                 v4i B[NSUB];
                 read_ops(bb, A, B, Sr[u]);
@@ -450,7 +480,6 @@ __global__ __launch_bounds__(256) void mfma_dma_kernel(DotArgs a, MatGeom g) {
         }
     }
     if (g.nb % 2 == 0) epi_blk(g.nb - 1, Dr[1], Sr[1]);   // the last block's epilogue did not run in the loop
-    wait_vm<0>();   // the clamped copies past the end land before the workgroup can exit
 
     // per-row activation scale (EPI_ROW / EPI_GRP) of each accumulator row
     float v[NSUB][16];
@@ -523,13 +552,20 @@ static void launch_mfma_p(const DotArgs &a, const MatGeom &g, int grid_tiles, hi
     hipLaunchKernelGGL((mfma_kernel<W4, EPI, GATEUP, NSUB, PD>), grid, dim3(256), lds, st, a, g, a.xq, a.sx);
 }
 
+// stages plus (per-32 activation scales) the tile's scales
+template <bool W4, int EPI, int PD>
+static size_t mfma_dma_lds(const MatGeom &g) {
+    return (size_t)(PD + 2) * DmaStage<W4>::BYTES + (EPI == EPI_B32 ? (size_t)g.nb * 32 * sizeof(float) : 0);
+}
+constexpr int DMA_PD_W4 = 6, DMA_PD_W8 = 3;
+
 template <bool W4, int EPI, bool GATEUP, int PD>
 static void launch_mfma_dma(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
     constexpr int NSUB = 2;
     const int ch_per_wg = GATEUP ? 4 * 32 : 4 * 32 * NSUB;
     const int span = GATEUP ? ((g.O + 31) & ~31) : g.O;
     dim3 grid((unsigned)((span + ch_per_wg - 1) / ch_per_wg), (unsigned)grid_tiles);
-    const size_t lds = (size_t)4 * (PD + 2) * DmaStage<W4, EPI>::BYTES;
+    const size_t lds = mfma_dma_lds<W4, EPI, PD>(g);
     auto kern = mfma_dma_kernel<W4, EPI, GATEUP, NSUB, PD>;
     static size_t attr_set = 64 * 1024;
     if (lds > attr_set &&
@@ -552,8 +588,11 @@ static void launch_mfma_t(const DotArgs &a, const MatGeom &g, int grid_tiles, hi
     // int8 weights carry twice the bytes per MFMA: the register-prefetch
     // kernel already streams them near its limit, and their larger stages
     // leave the staged kernel a shallower pipeline (measured slower)
-    if (!a.dots && (m == 1 || (m < 0 && W4 && a.mfma_stream))) {
-        launch_mfma_dma<W4, EPI, GATEUP, W4 ? 5 : 3>(a, g, grid_tiles, st);
+    constexpr int PD = W4 ? DMA_PD_W4 : DMA_PD_W8;
+    // two workgroups per CU need at most 80 KB each
+    const bool fits = mfma_dma_lds<W4, EPI, PD>(g) <= 80 * 1024;
+    if (!a.dots && fits && (m == 1 || (m < 0 && W4 && a.mfma_stream))) {
+        launch_mfma_dma<W4, EPI, GATEUP, PD>(a, g, grid_tiles, st);
         return;
     }
     launch_mfma_p<W4, EPI, GATEUP, 2>(a, g, grid_tiles, st);   // two blocks ahead: deeper costs occupancy
