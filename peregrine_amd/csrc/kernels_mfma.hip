@@ -557,7 +557,9 @@ template <bool W4, int EPI, int PD>
 static size_t mfma_dma_lds(const MatGeom &g) {
     return (size_t)(PD + 2) * DmaStage<W4>::BYTES + (EPI == EPI_B32 ? (size_t)g.nb * 32 * sizeof(float) : 0);
 }
-constexpr int DMA_PD_W4 = 6, DMA_PD_W8 = 3;
+// blocks in flight: gate/up (long K) goes deep; down (K = I, 48-64 blocks)
+// fits three workgroups per CU with shallower stages (both measured best)
+constexpr int DMA_PD_GU_W4 = 6, DMA_PD_DN_W4 = 3, DMA_PD_W8 = 3;
 
 template <bool W4, int EPI, bool GATEUP, int PD>
 static void launch_mfma_dma(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
@@ -588,7 +590,7 @@ static void launch_mfma_t(const DotArgs &a, const MatGeom &g, int grid_tiles, hi
     // int8 weights carry twice the bytes per MFMA: the register-prefetch
     // kernel already streams them near its limit, and their larger stages
     // leave the staged kernel a shallower pipeline (measured slower)
-    constexpr int PD = W4 ? DMA_PD_W4 : DMA_PD_W8;
+    constexpr int PD = W4 ? (GATEUP ? DMA_PD_GU_W4 : DMA_PD_DN_W4) : DMA_PD_W8;
     // two workgroups per CU need at most 80 KB each
     const bool fits = mfma_dma_lds<W4, EPI, PD>(g) <= 80 * 1024;
     if (!a.dots && fits && (m == 1 || (m < 0 && W4 && a.mfma_stream))) {
