@@ -230,7 +230,6 @@ struct DotArgs {   // shared by the GEMV and MFMA arms
     int act_identity;                                                   // activation row = r (down proj)
     int act_zero;                                                       // activation row = 0 (one token)
     int n_rows_fixed;                                                   // >= 0: row count known on the host
-    int mfma_stream;                                                    // MFMA arm: few rows per expert (LDS-staged kernel)
     long long *trace;                                                   // optional phase timestamps (tests/tuning)
     RouteArgs route;                                                    // gate/up GEMV: logits != null -> fused router
 };

@@ -576,9 +576,9 @@ static void launch_mfma_dma(const DotArgs &a, const MatGeom &g, int grid_tiles, 
     hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, a, g);
 }
 
-// COLI_HIP_MFMA_DMA: -1 (default) LDS-staged for weight-streaming int4
-// dispatches (few rows per expert), register prefetch otherwise; 0 / 1 force
-// one kernel (A/B measurement).
+// COLI_HIP_MFMA_DMA: -1 (default) the LDS-staged kernel wherever its stages
+// fit (two workgroups per CU), 0 / 1 force one kernel (A/B measurement). The
+// register-prefetch kernel also serves the per-block dot dump.
 static int mfma_mode() {
     static const int m = getenv("COLI_HIP_MFMA_DMA") ? atoi(getenv("COLI_HIP_MFMA_DMA")) : -1;
     return m;
@@ -587,13 +587,9 @@ static int mfma_mode() {
 template <bool W4, int EPI, bool GATEUP>
 static void launch_mfma_t(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
     const int m = mfma_mode();
-    // int8 weights carry twice the bytes per MFMA: the register-prefetch
-    // kernel already streams them near its limit, and their larger stages
-    // leave the staged kernel a shallower pipeline (measured slower)
     constexpr int PD = W4 ? (GATEUP ? DMA_PD_GU_W4 : DMA_PD_DN_W4) : DMA_PD_W8;
-    // two workgroups per CU need at most 80 KB each
     const bool fits = mfma_dma_lds<W4, EPI, PD>(g) <= 80 * 1024;
-    if (!a.dots && fits && (m == 1 || (m < 0 && W4 && a.mfma_stream))) {
+    if (!a.dots && m != 0 && fits) {
         launch_mfma_dma<W4, EPI, GATEUP, PD>(a, g, grid_tiles, st);
         return;
     }

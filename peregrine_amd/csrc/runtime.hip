@@ -470,7 +470,6 @@ struct DispatchOpts {
     bool act_zero = false;      // every row reads activation row 0 (one token)
     int n_rows_fixed = -1;      // row count known on the host
     RouteArgs route{};          // one token: router + quant fused into the gate/up GEMV
-    bool mfma_stream = false;   // MFMA arm: under one 32-row tile per expert on average (weight streaming)
 };
 
 // The kernel sequence of one dispatch after the activations are on the
@@ -504,7 +503,6 @@ void run_experts(Ctx *c, Prof &prof, const ExpertDesc *desc, const RowPlan &plan
     da.act_zero = opt.act_zero ? 1 : 0;
     da.n_rows_fixed = opt.n_rows_fixed;
     da.route = opt.route;
-    da.mfma_stream = opt.mfma_stream ? 1 : 0;
     prof.mark(COLI_HIP_K_GATEUP);
     if (arm == COLI_HIP_ARM_GEMV)
         launch_gemv_gateup(da, gg, act, R_bound, c->stream);
@@ -645,7 +643,6 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
     plan.mt_rend = di + total + 2 * T;
     plan.counts = di + total + 3 * T;
     DispatchOpts opt;
-    opt.mfma_stream = total < MT_ROWS * count;
     run_experts(c, prof, (const ExpertDesc *)dm, plan, gg, gd, x_dev, total, true, total, T, ga, arm, s, opt);
     float *res = s.y;
     if (red) {
@@ -1158,7 +1155,6 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
         plan.mt_rend = t.mt_rend;
         plan.counts = t.hdr;
     }
-    opt.mfma_stream = R < MT_ROWS * std::min(E, R);   // rows per touched expert below one M-tile
     run_experts(c, prof, set->desc_dev, plan, gg, gd, x_dev, S, false, R, tmax, ga, arm, s, opt);
     prof.mark(COLI_HIP_K_COMBINE);
 #ifdef PHIP_STAGE_EXP

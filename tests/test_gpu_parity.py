@@ -95,8 +95,8 @@ def test_block_dots_bit_exact(hip, orc, arm, fmt):
     hip.set_act_group(32)
     hip.set_arm(arm)
     hip.set_debug_dots(dgu.ptr, ddn.ptr)
-    try:
-        hip.expert_group(gpu, rows, x, D)
+    try:   # with the dump on, the MFMA arm runs its register-prefetch kernel
+        y = hip.expert_group(gpu, rows, x, D)
     finally:
         hip.set_debug_dots(0, 0)
     gu = dgu.download(np.int32, (R, 2, I, nbd))
@@ -109,6 +109,7 @@ def test_block_dots_bit_exact(hip, orc, arm, fmt):
         _, h = orc.expert_swiglu(x[r0:r0 + n], *ora[e], 32, want_h=True)
         hq, _ = orc.quant_rows(h, 32)
         assert np.array_equal(dn[r0:r0 + n], orc.block_dots(hq, ora[e][2]))
+        assert np.array_equal(y[r0:r0 + n], orc.expert_swiglu(x[r0:r0 + n], *ora[e], 32))
         r0 += n
 
 
@@ -347,9 +348,8 @@ def test_moe_layer_fused_router_matches_oracle(hip, orc, S, arm, ga):
 @pytest.mark.parametrize("ga", [32, 0])
 @pytest.mark.parametrize("fmt,gs", FORMATS)
 def test_mfma_dense_and_streaming_dispatches(hip, orc, ga, fmt, gs):
-    """The MFMA arm picks its LDS-staged kernel when experts get fewer rows
-    than one 32-row tile on average and the register-prefetch kernel when they
-    get more: both dispatches equal the oracle bit for bit."""
+    """MFMA dispatches with many rows per expert (full 32-row tiles) and with
+    under two (ragged tiles) equal the oracle bit for bit."""
     say("mfma dense/streaming", ga, fmt, gs)
     rng = np.random.default_rng(610 + ga + fmt)
     for E, S, k in ((3, 64, 2), (16, 9, 3)):   # 43 rows per expert, then under 2
