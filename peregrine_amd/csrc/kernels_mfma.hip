@@ -557,9 +557,11 @@ template <bool W4, int EPI, int PD>
 static size_t mfma_dma_lds(const MatGeom &g) {
     return (size_t)(PD + 2) * DmaStage<W4>::BYTES + (EPI == EPI_B32 ? (size_t)g.nb * 32 * sizeof(float) : 0);
 }
-// blocks in flight: gate/up (long K) goes deep; down (K = I, 48-64 blocks)
-// fits three workgroups per CU with shallower stages (both measured best)
-constexpr int DMA_PD_GU_W4 = 6, DMA_PD_DN_W4 = 3, DMA_PD_W8 = 3;
+// Blocks in flight: three, when the stages and the tile's activation scales
+// fit three workgroups per CU (160 KB / 3), else six with two per CU (80 KB).
+// Measured: occupancy wins where it is available (configs 3, 4, all down
+// projections), depth where it is not (config 5's gate/up, K = 6144).
+constexpr int DMA_PD_SHALLOW = 3, DMA_PD_DEEP_W4 = 6, DMA_PD_W8 = 3;
 
 template <bool W4, int EPI, bool GATEUP, int PD>
 static void launch_mfma_dma(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
@@ -587,11 +589,16 @@ static int mfma_mode() {
 template <bool W4, int EPI, bool GATEUP>
 static void launch_mfma_t(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
     const int m = mfma_mode();
-    constexpr int PD = W4 ? (GATEUP ? DMA_PD_GU_W4 : DMA_PD_DN_W4) : DMA_PD_W8;
-    const bool fits = mfma_dma_lds<W4, EPI, PD>(g) <= 80 * 1024;
-    if (!a.dots && m != 0 && fits) {
-        launch_mfma_dma<W4, EPI, GATEUP, PD>(a, g, grid_tiles, st);
-        return;
+    if (!a.dots && m != 0) {
+        if (mfma_dma_lds<W4, EPI, DMA_PD_SHALLOW>(g) <= 160 * 1024 / 3) {
+            launch_mfma_dma<W4, EPI, GATEUP, DMA_PD_SHALLOW>(a, g, grid_tiles, st);
+            return;
+        }
+        constexpr int PD = W4 ? DMA_PD_DEEP_W4 : DMA_PD_W8;
+        if (mfma_dma_lds<W4, EPI, PD>(g) <= 80 * 1024) {
+            launch_mfma_dma<W4, EPI, GATEUP, PD>(a, g, grid_tiles, st);
+            return;
+        }
     }
     launch_mfma_p<W4, EPI, GATEUP, 2>(a, g, grid_tiles, st);   // two blocks ahead: deeper costs occupancy
 }
