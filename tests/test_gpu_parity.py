@@ -569,3 +569,40 @@ def test_experts_from_qt_container(hip, orc, fmt, tmp_path):
         ref = orc.expert_swiglu(x[r0:r0 + n], *ora[e], 0)
         assert np.array_equal(y[r0:r0 + n], ref), e
         r0 += n
+
+
+@pytest.mark.parametrize("S,arm", [(1, 2), (5, 0), (5, 2)])
+def test_limits_512_experts_top16(hip, orc, S, arm):
+    """The largest supported dispatch: 512 experts, top-16 (the router runs
+    16 logits per lane, the GEMV one-token path 16 rows, the table 16 slots),
+    with router logits and with given ids; past the limits the calls fail."""
+    say("limits", S, arm)
+    rng = np.random.default_rng(5120 + S + arm)
+    E, D, I, k = 512, 96, 64, 16
+    n_real = 24   # 512 table entries over 24 distinct uploaded experts
+    gpu, ora = _experts(rng, n_real, D, I, qt.FMT_I4G, 32, orc, hip)
+    eset = hip.ExpertSet([gpu[e % n_real] for e in range(E)])
+    ora_full = [ora[e % n_real] for e in range(E)]
+    x = rng.standard_normal((S, D)).astype(np.float32)
+    logits = synth.normal_logits(rng, S, E)
+    bx, bl = hip.DeviceBuffer.from_array(x), hip.DeviceBuffer.from_array(logits)
+    bids, bw, bout = hip.DeviceBuffer(S * k * 4), hip.DeviceBuffer(S * k * 4), hip.DeviceBuffer(S * D * 4)
+    hip.moe_forward_logits_dev(eset, bx.ptr, S, bl.ptr, k, bids.ptr, bw.ptr, bout.ptr, 32, arm)
+    hip.pipe_sync(0)
+    ids, w = orc.route_softmax_topk(logits, k)
+    assert np.array_equal(bids.download(np.int32, (S, k)), ids)
+    assert np.array_equal(bw.download(np.float32, (S, k)), w)
+    ref = orc.moe_forward(x, ids, w, ora_full, 32)
+    assert np.array_equal(bout.download(np.float32, (S, D)), ref)
+    # given ids (the second path), same result
+    hip.moe_forward_dev(eset, bx.ptr, S, bids.ptr, bw.ptr, k, bout.ptr, 32, arm)
+    hip.pipe_sync(0)
+    assert np.array_equal(bout.download(np.float32, (S, D)), ref)
+    # one past each limit is refused, with nothing launched
+    b17 = hip.DeviceBuffer(S * 17 * 4)
+    with pytest.raises(hip.HipError):
+        hip.moe_forward_logits_dev(eset, bx.ptr, S, bl.ptr, 17, b17.ptr, b17.ptr, bout.ptr, 32, arm)
+    big = hip.ExpertSet([gpu[e % n_real] for e in range(E + 1)])
+    bl2 = hip.DeviceBuffer.from_array(synth.normal_logits(rng, S, E + 1))
+    with pytest.raises(hip.HipError):
+        hip.moe_forward_logits_dev(big, bx.ptr, S, bl2.ptr, k, bids.ptr, bw.ptr, bout.ptr, 32, arm)
