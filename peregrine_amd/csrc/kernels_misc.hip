@@ -498,7 +498,6 @@ __global__ __launch_bounds__(1024) void build_table_kernel(const int *ids, int S
     __shared__ short sid[TBL_MAXN];
     __shared__ int first[TBL_MAXE], cnt[TBL_MAXE], rank[TBL_MAXE], fill[TBL_MAXE], uex[TBL_MAXE];
     __shared__ unsigned long long mask[TBL_MAXE * 4];   // [e][up to 4 words]: one pass's tokens
-    __shared__ int cpos[1024];
     __shared__ int scan_tmp[32];
     __shared__ int s_nu, s_carry[2];
     const int tid = threadIdx.x, nth = blockDim.x;
@@ -585,34 +584,44 @@ __global__ __launch_bounds__(1024) void build_table_kernel(const int *ids, int S
         t.hdr[0] = t.hdr[1] = t.hdr[2] = t.hdr[3] = 0;
     }
     __syncthreads();
-    // Stable placement, TPP tokens per pass (one thread per (token, slot)
-    // entry): an entry's rank among its expert's rows in the pass = earlier
-    // tokens of the pass with the same expert, a popcount over the expert's
-    // per-pass token mask (TPP/64 words).
-    const int TPP = min(256, (nth / k) & ~63);   // k <= 16 keeps this >= 64
+    // Stable placement, TPP tokens per pass (up to two (token, slot) entries
+    // per thread): an entry's rank among its expert's rows in the pass =
+    // earlier tokens of the pass with the same expert, a popcount over the
+    // expert's per-pass token mask (TPP/64 words).
+    constexpr int EPT = 2;
+    const int TPP = min(256, (EPT * nth / k) & ~63);   // k <= 16 keeps this >= 64
     const int W = TPP >> 6;
     for (int c0 = 0; c0 < S; c0 += TPP) {
-        const int i = c0 * k + tid;
-        const bool mine = tid < TPP * k && i < N;
-        int e = -1, tok = 0;
-        if (mine) {
-            e = id_at(i);
-            tok = i / k - c0;
-            if (e >= 0) atomicOr(&mask[e * 4 + (tok >> 6)], 1ull << (tok & 63));
+        int ev[EPT], tokv[EPT], rv[EPT];
+        bool minev[EPT];
+#pragma unroll
+        for (int q = 0; q < EPT; q++) {
+            const int slot = tid + q * nth;
+            const int i = c0 * k + slot;
+            minev[q] = slot < TPP * k && i < N;
+            ev[q] = -1;
+            tokv[q] = 0;
+            if (minev[q]) {
+                ev[q] = id_at(i);
+                tokv[q] = i / k - c0;
+                if (ev[q] >= 0) atomicOr(&mask[ev[q] * 4 + (tokv[q] >> 6)], 1ull << (tokv[q] & 63));
+            }
         }
         __syncthreads();
-        if (mine) {
-            int r = -1;
-            if (e >= 0) {
+#pragma unroll
+        for (int q = 0; q < EPT; q++) {
+            rv[q] = -1;
+            if (minev[q] && ev[q] >= 0) {
+                const int i = c0 * k + tid + q * nth, e = ev[q], tok = tokv[q];
                 const unsigned long long *m = &mask[e * 4];
                 int rk = __popcll(m[tok >> 6] & ((1ull << (tok & 63)) - 1ull));
                 for (int w = 0; w < (tok >> 6); w++) rk += __popcll(m[w]);
-                r = fill[e] + rk;
+                const int r = fill[e] + rk;
                 t.row_tok[r] = i / k;
                 t.row_kk[r] = i % k;
                 t.row_exp[r] = e;
+                rv[q] = r;
             }
-            cpos[tid] = r;
         }
         __syncthreads();
         for (int e2 = tid; e2 < E; e2 += nth) {
@@ -626,7 +635,10 @@ __global__ __launch_bounds__(1024) void build_table_kernel(const int *ids, int S
         // the token's rows in union (rank) order: an entry's slot is the
         // number of the token's valid entries with a lower union rank; the
         // invalid entries fill the tail in slot order
-        if (mine) {
+#pragma unroll
+        for (int q = 0; q < EPT; q++) {
+            if (!minev[q]) continue;
+            const int i = c0 * k + tid + q * nth, e = ev[q];
             const int sx = i / k, kk = i % k;
             const int ur = e >= 0 ? rank[e] : INT_MAX;
             int p = 0, nv = 0, inv_before = 0;
@@ -640,7 +652,7 @@ __global__ __launch_bounds__(1024) void build_table_kernel(const int *ids, int S
                 }
             }
             const size_t at = (size_t)sx * k + (e >= 0 ? p : nv + inv_before);
-            t.tok_rows[at] = e >= 0 ? cpos[tid] : -1;
+            t.tok_rows[at] = e >= 0 ? rv[q] : -1;
             t.tok_kk[at] = e >= 0 ? kk : 0;
         }
         __syncthreads();
