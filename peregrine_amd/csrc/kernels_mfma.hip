@@ -558,10 +558,12 @@ static size_t mfma_dma_lds(const MatGeom &g) {
     return (size_t)(PD + 2) * DmaStage<W4>::BYTES + (EPI == EPI_B32 ? (size_t)g.nb * 32 * sizeof(float) : 0);
 }
 // Blocks in flight: three, when the stages and the tile's activation scales
-// fit three workgroups per CU (160 KB / 3), else six with two per CU (80 KB).
-// Measured: occupancy wins where it is available (configs 3, 4, all down
-// projections), depth where it is not (config 5's gate/up, K = 6144).
-constexpr int DMA_PD_SHALLOW = 3, DMA_PD_DEEP_W4 = 6, DMA_PD_W8 = 3;
+// fit three workgroups per CU (160 KB / 3); else two, if that fits three per
+// CU; else six with two per CU (80 KB). Measured: occupancy wins over depth
+// (configs 3, 4 and every down projection at three; config 5's int4 gate/up,
+// K = 6144, 806 us at two blocks and three per CU against 868 us at six and
+// two per CU).
+constexpr int DMA_PD_SHALLOW = 3, DMA_PD_NARROW = 2, DMA_PD_DEEP_W4 = 6, DMA_PD_W8 = 3;
 
 template <bool W4, int EPI, bool GATEUP, int PD>
 static void launch_mfma_dma(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
@@ -592,6 +594,10 @@ static void launch_mfma_t(const DotArgs &a, const MatGeom &g, int grid_tiles, hi
     if (!a.dots && m != 0) {
         if (mfma_dma_lds<W4, EPI, DMA_PD_SHALLOW>(g) <= 160 * 1024 / 3) {
             launch_mfma_dma<W4, EPI, GATEUP, DMA_PD_SHALLOW>(a, g, grid_tiles, st);
+            return;
+        }
+        if (mfma_dma_lds<W4, EPI, DMA_PD_NARROW>(g) <= 160 * 1024 / 3) {
+            launch_mfma_dma<W4, EPI, GATEUP, DMA_PD_NARROW>(a, g, grid_tiles, st);
             return;
         }
         constexpr int PD = W4 ? DMA_PD_DEEP_W4 : DMA_PD_W8;

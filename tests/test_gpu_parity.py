@@ -359,6 +359,22 @@ def test_mfma_dense_and_streaming_dispatches(hip, orc, ga, fmt, gs):
         assert np.array_equal(out, ref), (E, S, k, nerr(out, ref))
 
 
+@pytest.mark.parametrize("fmt,D", [(qt.FMT_I4G, 5120), (qt.FMT_I4G, 6400), (qt.FMT_I4G, 7680), (qt.FMT_I4G, 8320),
+                                   (qt.FMT_I8G, 768), (qt.FMT_I8G, 2048), (qt.FMT_I8G, 5120), (qt.FMT_I8G, 8320)])
+def test_mfma_staging_tiers(hip, orc, fmt, D):
+    """Per-32 activation scales with a hidden size at each gate/up staging
+    tier of the MFMA arm: three blocks ahead at three workgroups per CU, two
+    ahead at three, the deep tier at two, and the register-prefetch kernel
+    past them; bit-identical to the oracle."""
+    say("mfma tiers", fmt, D)
+    rng = np.random.default_rng(720 + D + fmt)
+    E, I, S, k = 3, 64, 40, 2
+    gpu, ora, eset, x, logits = _layer_case(hip, orc, rng, E, D, I, S, k, fmt=fmt)
+    out, ids, w = _run_layer(hip, eset, x, logits, k, 32, 0)
+    ref = orc.moe_forward(x, ids, w, ora, 32)
+    assert np.array_equal(out, ref), nerr(out, ref)
+
+
 def test_moe_layer_arms_agree_and_repeat(hip, orc):
     say("arms agree")
     rng = np.random.default_rng(77)
