@@ -260,5 +260,8 @@ struct TableOut {
     int *mt_exp, *mt_row0, *mt_rend;  // [Tmax]
 };
 void launch_synth_fill(void *dst, size_t n, int kind, float a, float b, uint64_t seed, hipStream_t st);
-void launch_build_table(const int *ids, int S, int k, int E, const TableOut &t, int tmax, hipStream_t st);
+// work: table_work_ints(S, k, E) ints of device scratch, fully rewritten by every call
+size_t table_work_ints(int S, int k, int E);
+void launch_build_table(const int *ids, int S, int k, int E, const TableOut &t, int tmax, int *work,
+                        hipStream_t st);
 }  // namespace phip

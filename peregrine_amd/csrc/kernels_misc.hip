@@ -464,91 +464,80 @@ void launch_route_softmax(const float *logits, int S, int E, int k, int *ids, fl
 // Expert-offset table, built on the device from router output, in the order
 // peregrine's moe_forward uses (peregrine-model/src/mlp.rs:62-104):
 //   experts in batch-union order (first seen over s ascending, kk ascending,
-//   router.rs:420-445); an expert's rows in ascending token order; each token's
-//   contributions listed in union order (the order the scatter adds them).
-// Also emits the 32-row M-tile list the MFMA arm walks. One workgroup; every
-// step is a counting pass, so the result does not depend on thread timing.
-// The router ids are staged in LDS once; nothing written is read back.
-// Limits: E <= 512, k <= 16 (ids beyond TBL_MAXN are read from global).
+//   router.rs:420-445); an expert's rows in ascending (token, slot) order;
+//   each token's contributions listed in union order, ties in slot order
+//   (the order the scatter adds them).
+// Also emits the 32-row M-tile list the MFMA arm walks. Three launches over
+// chunks of whole tokens (at most 256 entries each): per-chunk counts, one
+// scan over experts and chunks, per-chunk placement. Every step is a
+// counting pass, so the result does not depend on thread timing.
+// Limits: E <= 512, k <= 16.
 // ---------------------------------------------------------------------------
+// Inclusive scan across a wavefront: shifts of 1, 2, 4 and 8 lanes inside
+// each row of 16 (DPP row_shr, zero fill), then the earlier rows' totals.
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);   // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);   // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);   // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);   // row_shr:8
+    const int r1 = __builtin_amdgcn_readlane(v, 15), r2 = __builtin_amdgcn_readlane(v, 31),
+              r3 = __builtin_amdgcn_readlane(v, 47);
+    const int row = (threadIdx.x & 63) >> 4;
+    return v + (row >= 1 ? r1 : 0) + (row >= 2 ? r2 : 0) + (row >= 3 ? r3 : 0);
+}
+
 // Exclusive scan of one int per thread across a workgroup of up to 1024
 // threads (wave scans, then a scan of the wave totals). Ends synchronised.
 __device__ int block_exclusive_scan(int v, int *tmp) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
-    int inc = v;
-    for (int off = 1; off < 64; off <<= 1) {
-        const int o = __shfl_up(inc, off);
-        if (lane >= off) inc += o;
-    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int inc = wave_inclusive_scan(v);
     __syncthreads();
     if (lane == 63) tmp[wave] = inc;
     __syncthreads();
     int wbase = 0;
     for (int w = 0; w < wave; w++) wbase += tmp[w];
-    (void)nw;
     __syncthreads();
     return wbase + inc - v;
 }
 
 constexpr int TBL_MAXE = 512;
-constexpr int TBL_MAXN = 16384;
+constexpr int TBL_CHUNK = 256;      // entries per chunk (whole tokens)
+constexpr int TBL_TILE = 12288;     // (expert, chunk) counts one scan pass holds in LDS
 
-__global__ __launch_bounds__(1024) void build_table_kernel(const int *ids, int S, int k, int E, TableOut t,
-                                                           int tmax) {
-    __shared__ short sid[TBL_MAXN];
-    __shared__ int first[TBL_MAXE], cnt[TBL_MAXE], rank[TBL_MAXE], fill[TBL_MAXE], uex[TBL_MAXE];
-    __shared__ unsigned long long mask[TBL_MAXE * 4];   // [e][up to 4 words]: one pass's tokens
-    __shared__ int scan_tmp[32];
-    __shared__ int s_nu, s_carry[2];
-    const int tid = threadIdx.x, nth = blockDim.x;
-    const int N = S * k;
-    const bool in_lds = N <= TBL_MAXN;
-    auto id_at = [&](int i) -> int {
-        const int e = in_lds ? (int)sid[i] : ids[i];
-        return (e >= 0 && e < E) ? e : -1;
-    };
-    if (in_lds)
-        for (int i = tid; i < N; i += nth) sid[i] = (short)max(-1, min(ids[i], 32767));
-    for (int e = tid; e < E; e += nth) {
+// Per chunk g: cnt[g][e] = entries of expert e, first[g][e] = its first entry
+// index (INT_MAX when none). Every (g, e) is written, so nothing needs clearing.
+__global__ __launch_bounds__(TBL_CHUNK) void table_count_kernel(const int *ids, int N, int k, int E, int tpc,
+                                                                int *firstg, int *cntg) {
+    __shared__ int first[TBL_MAXE], cnt[TBL_MAXE];
+    const int g = blockIdx.x, tid = threadIdx.x;
+    for (int e = tid; e < E; e += TBL_CHUNK) {
         first[e] = INT_MAX;
         cnt[e] = 0;
-        mask[4 * e] = mask[4 * e + 1] = mask[4 * e + 2] = mask[4 * e + 3] = 0ull;
-        rank[e] = -1;
     }
     __syncthreads();
-    for (int i = tid; i < N; i += nth) {
-        const int e = id_at(i);
-        if (e >= 0) {
+    const int i = g * tpc * k + tid;
+    if (tid < tpc * k && i < N) {
+        const int e = ids[i];
+        if (e >= 0 && e < E) {
             atomicMin(&first[e], i);
             atomicAdd(&cnt[e], 1);
         }
     }
     __syncthreads();
-    // union rank = number of first occurrences before an expert's first
-    // occurrence: flag first occurrences, then one block-wide scan over the
-    // positions (each thread owns a contiguous run of them)
-    {
-        const int per = (N + nth - 1) / nth;
-        const int lo = min(N, tid * per), hi = min(N, lo + per);
-        int nf = 0;
-        for (int i = lo; i < hi; i++) {
-            const int e = id_at(i);
-            nf += (e >= 0 && first[e] == i);
-        }
-        int base = block_exclusive_scan(nf, scan_tmp);
-        for (int i = lo; i < hi; i++) {
-            const int e = id_at(i);
-            if (e >= 0 && first[e] == i) {
-                rank[e] = base;
-                uex[base] = e;
-                base++;
-            }
-        }
-        if (tid == nth - 1) s_nu = base;
+    for (int e = tid; e < E; e += TBL_CHUNK) {
+        firstg[(size_t)g * E + e] = first[e];
+        cntg[(size_t)g * E + e] = cnt[e];
     }
-    __syncthreads();
-    const int n_u = s_nu;
-    // row offsets and M-tile offsets in union order (block scans over experts)
+}
+
+// Row offsets and M-tile offsets in union order, the M-tile list and the
+// header, from the experts in union order (uex[0..n_u)) and their counts.
+// base_out[e]: the expert's first row. ubuf: LDS for 2 * (n_u + 1) ints.
+// Workgroup-wide; ends synchronised.
+__device__ void table_offsets(int n_u, const int *uex, const int *cnt, int *base_out, const TableOut &t, int tmax,
+                              int *scan_tmp, int *s_carry, int *ubuf) {
+    const int tid = threadIdx.x, nth = blockDim.x;
+    int *offs = ubuf, *mts = ubuf + n_u + 1;   // per union rank: first row, first M tile
     for (int u0 = 0; u0 < n_u; u0 += nth) {
         const int u = u0 + tid;
         const int c = u < n_u ? cnt[uex[u]] : 0;
@@ -556,15 +545,14 @@ __global__ __launch_bounds__(1024) void build_table_kernel(const int *ids, int S
         const int mt = block_exclusive_scan((c + MT_ROWS - 1) / MT_ROWS, scan_tmp) + (u0 ? s_carry[1] : 0);
         if (u < n_u) {
             const int e = uex[u];
-            fill[e] = off;
+            base_out[e] = off;
+            offs[u] = off;
+            mts[u] = mt;
             t.uexp[u] = e;
             t.off[u] = off;
-            for (int j = 0; j < (c + MT_ROWS - 1) / MT_ROWS && mt + j < tmax; j++) {
-                t.mt_exp[mt + j] = e;
-                t.mt_row0[mt + j] = off + MT_ROWS * j;
-                t.mt_rend[mt + j] = off + c;
-            }
             if (u == n_u - 1) {
+                offs[n_u] = off + c;
+                mts[n_u] = mt + (c + MT_ROWS - 1) / MT_ROWS;
                 t.off[n_u] = off + c;
                 t.hdr[0] = off + c;
                 t.hdr[1] = mt + (c + MT_ROWS - 1) / MT_ROWS;
@@ -579,88 +567,261 @@ __global__ __launch_bounds__(1024) void build_table_kernel(const int *ids, int S
         }
         __syncthreads();
     }
-    if (n_u == 0 && tid == 0) {
-        t.off[0] = 0;
-        t.hdr[0] = t.hdr[1] = t.hdr[2] = t.hdr[3] = 0;
+    if (n_u == 0) {
+        if (tid == 0) {
+            t.off[0] = 0;
+            t.hdr[0] = t.hdr[1] = t.hdr[2] = t.hdr[3] = 0;
+        }
+        __syncthreads();
+        return;
+    }
+    // the M-tile list, one tile per thread: its expert is the last union
+    // rank whose first tile is at or before it (every present expert has one)
+    const int T = min(mts[n_u], tmax);
+    for (int q = tid; q < T; q += nth) {
+        int lo = 0, hi = n_u - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (mts[mid] <= q) lo = mid;
+            else hi = mid - 1;
+        }
+        t.mt_exp[q] = uex[lo];
+        t.mt_row0[q] = offs[lo] + MT_ROWS * (q - mts[lo]);
+        t.mt_rend[q] = offs[lo + 1];
     }
     __syncthreads();
-    // Stable placement, TPP tokens per pass (up to two (token, slot) entries
-    // per thread): an entry's rank among its expert's rows in the pass =
-    // earlier tokens of the pass with the same expert, a popcount over the
-    // expert's per-pass token mask (TPP/64 words).
-    constexpr int EPT = 2;
-    const int TPP = min(256, (EPT * nth / k) & ~63);   // k <= 16 keeps this >= 64
-    const int W = TPP >> 6;
-    for (int c0 = 0; c0 < S; c0 += TPP) {
-        int ev[EPT], tokv[EPT], rv[EPT];
-        bool minev[EPT];
-#pragma unroll
-        for (int q = 0; q < EPT; q++) {
-            const int slot = tid + q * nth;
-            const int i = c0 * k + slot;
-            minev[q] = slot < TPP * k && i < N;
-            ev[q] = -1;
-            tokv[q] = 0;
-            if (minev[q]) {
-                ev[q] = id_at(i);
-                tokv[q] = i / k - c0;
-                if (ev[q] >= 0) atomicOr(&mask[ev[q] * 4 + (tokv[q] >> 6)], 1ull << (tokv[q] & 63));
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int q = 0; q < EPT; q++) {
-            rv[q] = -1;
-            if (minev[q] && ev[q] >= 0) {
-                const int i = c0 * k + tid + q * nth, e = ev[q], tok = tokv[q];
-                const unsigned long long *m = &mask[e * 4];
-                int rk = __popcll(m[tok >> 6] & ((1ull << (tok & 63)) - 1ull));
-                for (int w = 0; w < (tok >> 6); w++) rk += __popcll(m[w]);
-                const int r = fill[e] + rk;
-                t.row_tok[r] = i / k;
-                t.row_kk[r] = i % k;
-                t.row_exp[r] = e;
-                rv[q] = r;
-            }
-        }
-        __syncthreads();
-        for (int e2 = tid; e2 < E; e2 += nth) {
-            int n = 0;
-            for (int w = 0; w < W; w++) {
-                n += __popcll(mask[e2 * 4 + w]);
-                mask[e2 * 4 + w] = 0ull;
-            }
-            fill[e2] += n;
-        }
-        // the token's rows in union (rank) order: an entry's slot is the
-        // number of the token's valid entries with a lower union rank; the
-        // invalid entries fill the tail in slot order
-#pragma unroll
-        for (int q = 0; q < EPT; q++) {
-            if (!minev[q]) continue;
-            const int i = c0 * k + tid + q * nth, e = ev[q];
-            const int sx = i / k, kk = i % k;
-            const int ur = e >= 0 ? rank[e] : INT_MAX;
-            int p = 0, nv = 0, inv_before = 0;
-            for (int k2 = 0; k2 < k; k2++) {
-                const int e2 = id_at(sx * k + k2);
-                if (e2 >= 0) {
-                    nv++;
-                    p += rank[e2] < ur;
-                } else if (k2 < kk) {
-                    inv_before++;
-                }
-            }
-            const size_t at = (size_t)sx * k + (e >= 0 ? p : nv + inv_before);
-            t.tok_rows[at] = e >= 0 ? rv[q] : -1;
-            t.tok_kk[at] = e >= 0 ? kk : 0;
-        }
-        __syncthreads();
-    }
 }
 
-void launch_build_table(const int *ids, int S, int k, int E, const TableOut &t, int tmax, hipStream_t st) {
-    hipLaunchKernelGGL(build_table_kernel, dim3(1), dim3(1024), 0, st, ids, S, k, E, t, tmax);
+// One workgroup: per expert, the first occurrence (min over chunks), the
+// count, and in place of cnt[g][e] its exclusive prefix over chunks; then
+// the union ranks (order of first occurrence), row offsets, M tiles and the
+// header. ebase[e] = the expert's first row, erank[e] = its union rank.
+__global__ __launch_bounds__(1024) void table_scan_kernel(int E, int G, const int *firstg, int *cntg, int *erank,
+                                                          int *ebase, TableOut t, int tmax) {
+    __shared__ int tile[TBL_TILE];
+    __shared__ __attribute__((aligned(16))) int first[TBL_MAXE];
+    __shared__ int cnt[TBL_MAXE], uex[TBL_MAXE];
+    __shared__ int scan_tmp[32];
+    __shared__ int s_carry[2], s_nu;
+    const int tid = threadIdx.x, nth = blockDim.x;
+    for (int e = tid; e < ((E + 3) & ~3); e += nth) {
+        first[e] = INT_MAX;
+        cnt[e] = 0;
+    }
+    if (tid == 0) s_nu = 0;
+    __syncthreads();
+    // passes over (chunk range, expert batch) tiles: load every count of the
+    // tile at once (one memory latency per pass), then one thread per expert
+    // walks its column of the tile; the running total stays in cnt[e]
+    const int EB = min(E, nth), GW = max(1, TBL_TILE / EB);
+    for (int g0 = 0; g0 < G; g0 += GW) {
+        const int ng = min(GW, G - g0);
+        for (int e0 = 0; e0 < E; e0 += EB) {
+            const int ne = min(EB, E - e0);
+            // all of a thread's loads first (at most TBL_TILE / nth each), then
+            // the LDS work, so the loads overlap
+            constexpr int PER = (TBL_TILE + 1023) / 1024;
+            int cv[PER], fv[PER];
+#pragma unroll
+            for (int j = 0; j < PER; j++) {
+                const int q = tid + j * nth;
+                cv[j] = 0;
+                fv[j] = INT_MAX;
+                if (q < ne * ng) {
+                    const int el = q % ne, gl = q / ne;   // consecutive threads: consecutive experts of one chunk
+                    const size_t at = (size_t)(g0 + gl) * E + e0 + el;
+                    cv[j] = cntg[at];
+                    fv[j] = firstg[at];
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < PER; j++) {
+                const int q = tid + j * nth;
+                if (q < ne * ng) {
+                    tile[q] = cv[j];
+                    if (fv[j] != INT_MAX) atomicMin(&first[e0 + q % ne], fv[j]);
+                }
+            }
+            __syncthreads();
+            if (tid < ne) {
+                int run = cnt[e0 + tid];
+#pragma unroll 8
+                for (int gl = 0; gl < ng; gl++) {
+                    const int c = tile[gl * ne + tid];
+                    cntg[(size_t)(g0 + gl) * E + e0 + tid] = run;
+                    run += c;
+                }
+                cnt[e0 + tid] = run;
+            }
+            __syncthreads();
+        }
+    }
+    // union rank: experts present, ordered by first occurrence (distinct);
+    // four first occurrences per LDS read, several reads in flight
+    const int4 *f4 = (const int4 *)first;
+    for (int e = tid; e < E; e += nth) {
+        const int f = first[e];
+        int r = -1;
+        if (f != INT_MAX) {
+            r = 0;
+#pragma unroll 8
+            for (int q = 0; q < (E + 3) >> 2; q++) {
+                const int4 v = f4[q];
+                r += (v.x < f) + (v.y < f) + (v.z < f) + (v.w < f);
+            }
+            uex[r] = e;
+            atomicAdd(&s_nu, 1);
+        }
+        erank[e] = r;
+    }
+    __syncthreads();
+    table_offsets(s_nu, uex, cnt, ebase, t, tmax, scan_tmp, s_carry, tile);   // the tile is free again
+}
+
+// Entry (tok, kk) of expert e (-1: invalid) at row r: its place among the
+// token's rows, in union order with equal experts in slot order; invalid
+// entries fill the tail in slot order. tid_e: the token's k expert ids.
+__device__ __forceinline__ void table_token_slot(const int *tid_e, int tok, int kk, int k, int e, int r,
+                                                 const int *rank, const TableOut &t) {
+    const int ur = e >= 0 ? rank[e] : INT_MAX;
+    int p = 0, nv = 0, inv_before = 0;
+    for (int k2 = 0; k2 < k; k2++) {
+        const int e2 = tid_e[k2];
+        if (e2 >= 0) {
+            nv++;
+            const int r2 = rank[e2];
+            p += r2 < ur || (r2 == ur && k2 < kk);
+        } else if (k2 < kk) {
+            inv_before++;
+        }
+    }
+    const size_t at = (size_t)tok * k + (e >= 0 ? p : nv + inv_before);
+    t.tok_rows[at] = r;
+    t.tok_kk[at] = e >= 0 ? kk : 0;
+}
+
+// Per chunk g: an entry's row = its expert's first row + the expert's
+// entries in earlier chunks + its earlier entries in this chunk (a popcount
+// over the expert's entry mask); then its place among its token's rows.
+__global__ __launch_bounds__(TBL_CHUNK) void table_place_kernel(const int *ids, int N, int k, int E, int tpc,
+                                                                const int *pref, const int *erank,
+                                                                const int *ebase, TableOut t) {
+    constexpr int MW = TBL_CHUNK / 64;
+    __shared__ int rank[TBL_MAXE], base[TBL_MAXE];
+    __shared__ unsigned long long mask[TBL_MAXE * MW];
+    __shared__ int sid[TBL_CHUNK];
+    const int g = blockIdx.x, tid = threadIdx.x;
+    for (int e = tid; e < E; e += TBL_CHUNK) {
+        const int r = erank[e];
+        rank[e] = r;
+        base[e] = r >= 0 ? ebase[e] + pref[(size_t)g * E + e] : 0;   // absent experts: no base was written
+#pragma unroll
+        for (int w = 0; w < MW; w++) mask[e * MW + w] = 0ull;
+    }
+    const int i0 = g * tpc * k;
+    const int n = min(N - i0, tpc * k);
+    int e = -1;
+    if (tid < n) {
+        e = ids[i0 + tid];
+        if (e < 0 || e >= E) e = -1;
+        sid[tid] = e;
+    }
+    __syncthreads();
+    if (e >= 0) atomicOr(&mask[e * MW + (tid >> 6)], 1ull << (tid & 63));
+    __syncthreads();
+    if (tid >= n) return;
+    const int i = i0 + tid, tok = i / k, kk = i % k;
+    int r = -1;
+    if (e >= 0) {
+        const unsigned long long *m = &mask[e * MW];
+        int rk = __popcll(m[tid >> 6] & ((1ull << (tid & 63)) - 1ull));
+        for (int w = 0; w < (tid >> 6); w++) rk += __popcll(m[w]);
+        r = base[e] + rk;
+        t.row_tok[r] = tok;
+        t.row_kk[r] = kk;
+        t.row_exp[r] = e;
+    }
+    table_token_slot(sid + (tid - kk), tok, kk, k, e, r, rank, t);   // chunks hold whole tokens
+}
+
+// Batches of at most TBL_SMALL entries in one launch, one entry per thread:
+// union ranks from a scan over the first occurrences, an entry's rank among
+// its expert's rows from a popcount over the expert's entry mask.
+constexpr int TBL_SMALL = 512;
+__global__ __launch_bounds__(TBL_SMALL) void table_small_kernel(const int *ids, int N, int k, int E, TableOut t,
+                                                                int tmax) {
+    constexpr int MW = TBL_SMALL / 64;
+    __shared__ int sid[TBL_SMALL];
+    __shared__ unsigned long long mask[TBL_MAXE * MW];
+    __shared__ int first[TBL_MAXE], cnt[TBL_MAXE], uex[TBL_MAXE], rank[TBL_MAXE], base[TBL_MAXE];
+    __shared__ int ubuf[2 * (TBL_MAXE + 1)];
+    __shared__ int scan_tmp[32];
+    __shared__ int s_carry[2], s_nu;
+    const int tid = threadIdx.x;
+    for (int e = tid; e < E; e += TBL_SMALL) {
+        first[e] = INT_MAX;
+        cnt[e] = 0;
+        rank[e] = -1;
+#pragma unroll
+        for (int w = 0; w < MW; w++) mask[e * MW + w] = 0ull;
+    }
+    int e = -1;
+    if (tid < N) {
+        e = ids[tid];
+        if (e < 0 || e >= E) e = -1;
+        sid[tid] = e;
+    }
+    __syncthreads();
+    if (e >= 0) {
+        atomicMin(&first[e], tid);
+        atomicAdd(&cnt[e], 1);
+        atomicOr(&mask[e * MW + (tid >> 6)], 1ull << (tid & 63));
+    }
+    __syncthreads();
+    const bool opens = e >= 0 && first[e] == tid;   // the expert's first entry
+    const int u = block_exclusive_scan(opens, scan_tmp);
+    if (opens) {
+        rank[e] = u;
+        uex[u] = e;
+    }
+    if (tid == TBL_SMALL - 1) s_nu = u + opens;
+    __syncthreads();
+    table_offsets(s_nu, uex, cnt, base, t, tmax, scan_tmp, s_carry, ubuf);
+    if (tid >= N) return;
+    const int tok = tid / k, kk = tid % k;
+    int r = -1;
+    if (e >= 0) {
+        const unsigned long long *m = &mask[e * MW];
+        int rk = __popcll(m[tid >> 6] & ((1ull << (tid & 63)) - 1ull));
+        for (int w = 0; w < (tid >> 6); w++) rk += __popcll(m[w]);
+        r = base[e] + rk;
+        t.row_tok[r] = tok;
+        t.row_kk[r] = kk;
+        t.row_exp[r] = e;
+    }
+    table_token_slot(sid + (tid - kk), tok, kk, k, e, r, rank, t);
+}
+
+int table_chunks(int S, int k) {
+    const int tpc = TBL_CHUNK / k;
+    return (S + tpc - 1) / tpc;
+}
+size_t table_work_ints(int S, int k, int E) { return 2 * (size_t)table_chunks(S, k) * E + 2 * (size_t)E; }
+
+void launch_build_table(const int *ids, int S, int k, int E, const TableOut &t, int tmax, int *work,
+                        hipStream_t st) {
+    const int tpc = TBL_CHUNK / k, G = table_chunks(S, k), N = S * k;
+    if (N <= TBL_SMALL) {
+        hipLaunchKernelGGL(table_small_kernel, dim3(1), dim3(TBL_SMALL), 0, st, ids, N, k, E, t, tmax);
+        return;
+    }
+    int *firstg = work, *cntg = firstg + (size_t)G * E, *erank = cntg + (size_t)G * E, *ebase = erank + E;
+    if (G > 0)
+        hipLaunchKernelGGL(table_count_kernel, dim3(G), dim3(TBL_CHUNK), 0, st, ids, N, k, E, tpc, firstg, cntg);
+    hipLaunchKernelGGL(table_scan_kernel, dim3(1), dim3(1024), 0, st, E, G, firstg, cntg, erank, ebase, t, tmax);
+    if (G > 0)
+        hipLaunchKernelGGL(table_place_kernel, dim3(G), dim3(TBL_CHUNK), 0, st, ids, N, k, E, tpc, cntg, erank, ebase,
+                           t);
 }
 
 // ---------------------------------------------------------------------------

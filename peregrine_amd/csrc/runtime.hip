@@ -1080,7 +1080,8 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
     const MatGeom &gg = set->gg, &gd = set->gd;
 
     // table layout in one buffer
-    const size_t n_int = 4 + (size_t)E + (E + 1) + 3 * (size_t)R + 2 * (size_t)R + 3 * (size_t)tmax;
+    const size_t n_int =
+        4 + (size_t)E + (E + 1) + 3 * (size_t)R + 2 * (size_t)R + 3 * (size_t)tmax + table_work_ints(S, k, E);
     Scratch s{};
     if (!reserve_rows(c, gg, gd, S, R, ga, &s) || !reserve(c, c->tbl, n_int * 4)) return 0;
     int *p = (int *)c->tbl.p;
@@ -1107,6 +1108,7 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
     p += tmax;
     t.mt_rend = p;
     p += tmax;
+    int *tbl_work = p;
     c->tbl_view = t;
     c->tbl_E = E;
     c->tbl_R = R;
@@ -1147,7 +1149,7 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
         opt.n_rows_fixed = k;
     } else {
         prof.mark(COLI_HIP_K_TABLE);
-        launch_build_table(ids_dev, S, k, E, t, tmax, c->stream);
+        launch_build_table(ids_dev, S, k, E, t, tmax, tbl_work, c->stream);
         plan.row_exp = t.row_exp;
         plan.row_act = t.row_tok;
         plan.mt_exp = t.mt_exp;

@@ -525,6 +525,35 @@ def test_expert_table_many_passes(hip, orc, S, k, E):
     assert np.array_equal(out[sub], ref[sub])
 
 
+@pytest.mark.parametrize("S,k,E", [(300, 6, 20), (40, 16, 5), (513, 3, 300), (600, 16, 512)])
+def test_expert_table_duplicate_and_invalid_ids(hip, orc, S, k, E):
+    """Caller-supplied ids with repeated experts inside a token and ids out of
+    range (skipped): table and layer equal the oracle's."""
+    say("table duplicate/invalid ids", S, k, E)
+    rng = np.random.default_rng(1300 + S + k)
+    D, I = 64, 32
+    n_exp = min(E, 24)
+    gpu, ora = _experts(rng, n_exp, D, I, qt.FMT_I4G, 32, orc, hip)
+    eset = hip.ExpertSet([gpu[e % n_exp] for e in range(E)])
+    ora_full = [ora[e % n_exp] for e in range(E)]
+    ids = rng.integers(-2, E + 2, size=(S, k)).astype(np.int32)
+    ids[::7, 1:] = ids[::7, :1]            # every seventh token: one expert in every slot
+    w = rng.random((S, k)).astype(np.float32)
+    x = rng.standard_normal((S, D)).astype(np.float32)
+    bx, bids, bw = hip.DeviceBuffer.from_array(x), hip.DeviceBuffer.from_array(ids), hip.DeviceBuffer.from_array(w)
+    bout = hip.DeviceBuffer(S * D * 4)
+    hip.moe_forward_dev(eset, bx.ptr, S, bids.ptr, bw.ptr, k, bout.ptr, 32, 0)
+    hip.pipe_sync(0)
+    out = bout.download(np.float32, (S, D))
+    t = hip.last_table(0, E, S * k)
+    o = orc.expert_table(ids, E)
+    assert t["n_u"] == o["n_u"] and np.array_equal(t["uexp"], o["uexp"]) and np.array_equal(t["off"], o["off"])
+    assert np.array_equal(t["row_tok"], o["row_tok"])
+    assert np.array_equal(t["tok_rows"].reshape(S, k), o["tok_rows"])
+    ref = orc.moe_forward(x, ids, w, ora_full, 32)
+    assert np.array_equal(out, ref), nerr(out, ref)
+
+
 @pytest.mark.parametrize("min_share,norm,scale", [(0.0, True, 2.5), (0.05, True, 1.0), (0.02, False, 1.7)])
 def test_sigmoid_router_matches_oracle(hip, orc, min_share, norm, scale):
     """The reference router (router.rs:52-170) on the device equals the
