@@ -126,6 +126,13 @@ int coli_hip_set_arm(int arm);
  * at least 256 workgroups; COLI_HIP_FUSED_ROUTE=0 in the environment turns the
  * automatic choice off), 0 never, 1 whenever eligible. */
 int coli_hip_set_fused_route(int mode);
+/* One-token layers on the GEMV arm: the down projection also applies the
+ * router weights in top-k order (one launch instead of down + combine; the
+ * same bits). Eligible for k <= 8 and K <= 1536 (the down projection's input
+ * width). -1 automatic (default: eligible and k <= 2), 0 never, 1 whenever
+ * eligible. COLI_HIP_FUSED_COMBINE=0 in the environment turns the automatic
+ * choice off. */
+int coli_hip_set_fused_combine(int mode);
 
 /* ---- NEW: device-resident MoE layer (inputs already in HBM) ---- */
 /* A fixed expert table: expert id e -> (gates[e], ups[e], downs[e]). */

@@ -251,6 +251,10 @@ void launch_route_quant(const float *logits, int S, int E, int k, int *ids, floa
                         const ExpertDesc *desc, ExpertDesc *row_desc, hipStream_t st);
 // LDS bytes one workgroup may use (device attribute), set at init.
 void set_lds_limit(int bytes);
+// one token: down GEMV + router-weighted combine in one launch (k rows in top-k order)
+bool gemv_down_combine_ok(const MatGeom &g, int k);
+void launch_gemv_down_combine(const DotArgs &a, const MatGeom &g, int act, int k, const float *w, float *out,
+                              hipStream_t st);
 
 struct TableOut {
     int *hdr;          // [4]: R, T, n_u, flags

@@ -439,6 +439,161 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemv_kernel(DotArgs a, MatGeom 
     }
 }
 
+// One token, down projection and combine in one launch. A workgroup owns 16
+// channels (half a weight tile) for all k slots; wave w streams slot w. Lane
+// l takes channel l % 16 and one quarter of K (blocks [qQ, qQ + Q), q = l / 16,
+// Q = ceil(nb / 4)), every block of the wave in flight at once. The slots'
+// activation rows and scales are staged in LDS by loads issued before the
+// weight loads (a wave's loads return in order). Lanes 0-15 then run each
+// channel's exact f32 chain in ascending block order, as the chain wave of
+// gemv_kernel does, taking the other quarters' (dot, factor) pairs by
+// cross-lane reads. The router-weighted sum runs in slot order,
+// out = (((0 + w0*y0) + w1*y1) + ...), the combine's order for one token
+// (its rows in top-k order), so the result equals the separate down and
+// combine launches bit for bit.
+constexpr int DC_MAXK = 8, DC_CH = 12, DC_XLD = 6;   // blocks per lane; 8-byte activation loads per thread
+constexpr int DC_MAXNB = 4 * DC_CH;                   // K <= 1536
+
+template <bool W4, int EPI>
+__global__ __launch_bounds__(64 * DC_MAXK) void gemv_down_combine_kernel(DotArgs a, MatGeom g, int k,
+                                                                         const float *wts, float *out) {
+    constexpr int BB = W4 ? 16 : 32, CH = DC_CH;
+    __shared__ __attribute__((aligned(16))) int8_t xl[DC_MAXK * DC_MAXNB * BLK];   // [k][nb * 32]
+    __shared__ float sxl[DC_MAXK * DC_MAXNB];                                     // [k][nsx]
+    __shared__ float comb[DC_MAXK * 16];
+    const int nb = g.nb, Kp = nb * BLK, Q = (nb + 3) >> 2;
+    const int nsx = EPI == EPI_B32 ? nb : 1;
+    const int tid = threadIdx.x, nth = blockDim.x, lane = tid & 63, r = tid >> 6;
+    const int qd = lane >> 4, ol = lane & 15;
+    // activation rows and scales: a fixed number of loads per thread, issued
+    // first (clamped; the extra ones repeat the last element)
+    const int nx8 = k * Kp / 8, nsxt = k * nsx;
+    uint2 xv[DC_XLD];
+#pragma unroll
+    for (int u = 0; u < DC_XLD; ++u) {
+        const int i = min(tid + u * nth, nx8 - 1), rr = i / (Kp / 8), off = i - rr * (Kp / 8);
+        xv[u] = *(const uint2 *)(a.xq + (size_t)rr * a.x_stride + (size_t)off * 8);
+    }
+    float sv0;
+    {
+        const int i = min(tid, nsxt - 1), rr = i / nsx;
+        sv0 = a.sx[(size_t)rr * a.sx_stride + (i - rr * nsx)];
+    }
+    const ExpertDesc *dsc = a.plan.row_desc ? &a.plan.row_desc[r] : &a.desc[a.plan.row_exp[r]];
+    const int sl = blockIdx.x, t = sl >> 1, row = (sl & 1) * 16 + ol;
+    const auto *wp = gptr(dsc->w[2] + ((size_t)t * nb * TILE_O + row) * BB);
+    const auto *sp = gptr(dsc->sc[2] + (size_t)t * g.ng * TILE_O + row);
+    const int bbeg = qd * Q;
+    WBlk<W4> wv[CH];
+    float sw[CH];
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {   // unconditional, clamped: one batch of loads
+        const int b = min(bbeg + j, nb - 1);
+        wv[j] = load_wblk<W4>((const uint8_t *)(wp + (size_t)b * (TILE_O * BB)));
+        if constexpr (EPI != EPI_ROW) sw[j] = __builtin_nontemporal_load(&sp[(size_t)grp_of(b, g.gshift) * TILE_O]);
+    }
+#pragma unroll
+    for (int u = 0; u < DC_XLD; ++u) {
+        const int i = tid + u * nth;
+        if (i < nx8) *(uint2 *)(xl + (size_t)i * 8) = xv[u];   // rows are packed at nb * 32 bytes
+    }
+    if (tid < nsxt) sxl[tid] = sv0;
+    __syncthreads();
+    const int *xr = (const int *)(xl + (size_t)r * Kp);
+    const float *sxr = sxl + (size_t)r * nsx;
+    // this lane's exact block dots and f32 factors
+    int dv[CH];
+    float fv[CH];
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+        const int b = min(bbeg + j, nb - 1);
+        int xb[8];
+        const int4 q0 = *(const int4 *)(xr + b * (BLK / 4)), q1 = *(const int4 *)(xr + b * (BLK / 4) + 4);
+        xb[0] = q0.x; xb[1] = q0.y; xb[2] = q0.z; xb[3] = q0.w;
+        xb[4] = q1.x; xb[5] = q1.y; xb[6] = q1.z; xb[7] = q1.w;
+        const int d16 = dot_wblk<W4>(wv[j], xb);
+        dv[j] = W4 ? (d16 >> 4) : d16;
+        if constexpr (EPI != EPI_ROW) {
+            const float s = W4 ? __fmul_rn(sw[j], 16.0f) : sw[j];   // W4 scale tables hold sw/16
+            fv[j] = EPI == EPI_B32 ? __fmul_rn(s, sxr[b]) : s;
+        } else {
+            fv[j] = 0.0f;
+        }
+    }
+    float facc = 0.0f;
+    int gsum = 0, isum = 0;
+    auto apply = [&](int b, int d, float f) {
+        if constexpr (EPI == EPI_ROW) {
+            isum += d;
+        } else if constexpr (EPI == EPI_B32) {
+            facc = __fmaf_rn(f, (float)d, facc);
+        } else {
+            gsum += d;
+            if (grp_end(b, g.gshift, nb)) {
+                facc = __fadd_rn(facc, __fmul_rn((float)gsum, f));
+                gsum = 0;
+            }
+        }
+    };
+    // quarters in order; every lane runs the chain, lanes 0-15 keep it
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        int dq[CH];
+        float fq[CH];
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            dq[j] = q == 0 ? dv[j] : __shfl(dv[j], ol + 16 * q);
+            fq[j] = q == 0 ? fv[j] : __shfl(fv[j], ol + 16 * q);
+        }
+#pragma unroll
+        for (int j = 0; j < CH; ++j)
+            if (j < Q && q * Q + j < nb) apply(q * Q + j, dq[j], fq[j]);
+    }
+    float v;
+    if constexpr (EPI == EPI_ROW) {
+        const float sc = W4 ? __fmul_rn(sp[0], 16.0f) : sp[0];   // per-row scale
+        v = __fmul_rn(__fmul_rn((float)isum, sc), sxr[0]);
+    } else if constexpr (EPI == EPI_GRP) {
+        v = __fmul_rn(facc, sxr[0]);
+    } else {
+        v = facc;
+    }
+    if (lane < 16) comb[r * 16 + ol] = v;
+    __syncthreads();
+    const int o = sl * 16 + tid;
+    if (tid < 16 && o < g.O) {
+        float acc = 0.0f;
+        for (int rr = 0; rr < k; ++rr) acc = __fadd_rn(acc, __fmul_rn(wts[rr], comb[rr * 16 + tid]));
+        out[o] = acc;
+    }
+}
+
+// whether the fused down + combine covers this shape: k slots, K blocks, and
+// every activation byte within the fixed per-thread loads (8 B each)
+bool gemv_down_combine_ok(const MatGeom &g, int k) {
+    return k >= 1 && k <= DC_MAXK && g.nb <= DC_MAXNB && g.nb * BLK / 8 <= DC_XLD * 64;
+}
+
+template <bool W4, int EPI>
+static void launch_dc(const DotArgs &a, const MatGeom &g, int k, const float *w, float *out, hipStream_t st) {
+    const dim3 grid((unsigned)((g.O + 15) / 16)), block((unsigned)(64 * k));
+    hipLaunchKernelGGL((gemv_down_combine_kernel<W4, EPI>), grid, block, 0, st, a, g, k, w, out);
+}
+
+void launch_gemv_down_combine(const DotArgs &a, const MatGeom &g, int act, int k, const float *w, float *out,
+                              hipStream_t st) {
+    const int epi = act == ACT_B32 ? EPI_B32 : (g.per_row ? EPI_ROW : EPI_GRP);
+    if (g.w4) {
+        if (epi == EPI_ROW) launch_dc<true, EPI_ROW>(a, g, k, w, out, st);
+        else if (epi == EPI_GRP) launch_dc<true, EPI_GRP>(a, g, k, w, out, st);
+        else launch_dc<true, EPI_B32>(a, g, k, w, out, st);
+    } else {
+        if (epi == EPI_ROW) launch_dc<false, EPI_ROW>(a, g, k, w, out, st);
+        else if (epi == EPI_GRP) launch_dc<false, EPI_GRP>(a, g, k, w, out, st);
+        else launch_dc<false, EPI_B32>(a, g, k, w, out, st);
+    }
+}
+
 static int g_lds_limit = 64 * 1024;
 void set_lds_limit(int bytes) { g_lds_limit = bytes > 0 ? bytes : 64 * 1024; }
 

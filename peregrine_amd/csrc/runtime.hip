@@ -197,6 +197,22 @@ int fused_route_mode() {
     return m;
 }
 
+// One-token down GEMV + combine in one launch: -1 automatic (k <= 2; with
+// more slots every weight block in flight at once streams slower than the
+// separate down GEMV's rounds: config 2, k = 8, 34.2 vs 32.5 us per layer;
+// config 1, k = 1, 15.2 vs 18.2 us), 0 never, 1 whenever eligible.
+// COLI_HIP_FUSED_COMBINE=0 in the environment sets 0 at first use.
+std::atomic<int> g_fused_combine{-2};
+bool fused_combine_on(int k) {
+    int m = g_fused_combine.load();
+    if (m == -2) {
+        const char *e = getenv("COLI_HIP_FUSED_COMBINE");
+        m = e && e[0] == '0' ? 0 : -1;
+        g_fused_combine.store(m);
+    }
+    return m == 1 || (m == -1 && k <= 2);
+}
+
 int forced_arm() {
     if (g_arm == -2) {
         const char *v = std::getenv("COLI_HIP_ARM");
@@ -470,6 +486,8 @@ struct DispatchOpts {
     bool act_zero = false;      // every row reads activation row 0 (one token)
     int n_rows_fixed = -1;      // row count known on the host
     RouteArgs route{};          // one token: router + quant fused into the gate/up GEMV
+    const float *combine_w = nullptr;   // one token: down + combine in one launch, weights [k]
+    float *combine_out = nullptr;       //   and the layer output [D]
 };
 
 // The kernel sequence of one dispatch after the activations are on the
@@ -533,7 +551,9 @@ void run_experts(Ctx *c, Prof &prof, const ExpertDesc *desc, const RowPlan &plan
 #ifdef PHIP_STAGE_EXP
     if (getenv("PHIP_STAGES") && atoi(getenv("PHIP_STAGES")) < 2) return;
 #endif
-    if (arm == COLI_HIP_ARM_GEMV) {
+    if (arm == COLI_HIP_ARM_GEMV && opt.combine_out) {
+        launch_gemv_down_combine(dd, gd, act, opt.n_rows_fixed, opt.combine_w, opt.combine_out, c->stream);
+    } else if (arm == COLI_HIP_ARM_GEMV) {
         launch_gemv_down(dd, gd, act, R_bound, c->stream);
     } else {
         launch_mfma_down(dd, gd, act, T_bound, c->stream);
@@ -954,6 +974,12 @@ int coli_hip_set_arm(int arm) {
     return 1;
 }
 
+int coli_hip_set_fused_combine(int mode) {
+    if (mode < -1 || mode > 1) return fail("fused combine mode must be -1, 0 or 1");
+    g_fused_combine.store(mode);
+    return 1;
+}
+
 int coli_hip_set_fused_route(int mode) {
     if (mode < -1 || mode > 1) return fail("fused route mode must be -1, 0 or 1");
     g_fused_route.store(mode);
@@ -1138,6 +1164,13 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
         launch_route_quant(logits_dev, S, E, k, ids_dev, w_dev, qa, set->desc_dev, rdesc, c->stream);
         opt.x_quantized = true;
     }
+    // one token: the down GEMV also applies the router weights (one launch
+    // fewer) when the k activation rows fit its LDS
+    const bool fuse_dc = one_token && fused_combine_on(k) && !g_dbg_dn && gemv_down_combine_ok(gd, k);
+    if (fuse_dc) {
+        opt.combine_w = w_dev;
+        opt.combine_out = out_dev;
+    }
     RowPlan plan{};
     if (one_token) {
         c->tbl_view.hdr = nullptr;
@@ -1162,8 +1195,11 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
 #ifdef PHIP_STAGE_EXP
     if (getenv("PHIP_STAGES") && atoi(getenv("PHIP_STAGES")) < 3) { prof.mark(-1); prof.finish(); return 1; }
 #endif
-    if (one_token)   // rows 0..k-1 of token 0, in top-k order
+    if (fuse_dc) {
+        // combined by the down GEMV
+    } else if (one_token) {   // rows 0..k-1 of token 0, in top-k order
         launch_combine_tok(out_dev, s.y, nullptr, nullptr, w_dev, 1, k, gd.O, s.ys, c->stream);
+    }
     else
         launch_combine_tok(out_dev, s.y, t.tok_rows, t.tok_kk, w_dev, S, k, gd.O, s.ys, c->stream);
     prof.mark(-1);

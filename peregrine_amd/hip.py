@@ -350,6 +350,13 @@ def set_fused_route(mode: int) -> None:
         raise HipError("coli_hip_set_fused_route failed")
 
 
+def set_fused_combine(mode: int) -> None:
+    """One token on the GEMV arm, down projection and combine in one launch:
+    -1 automatic (k <= 2), 0 never, 1 whenever eligible (k <= 8, K <= 1536)."""
+    if lib.coli_hip_set_fused_combine(mode) != 1:
+        raise HipError("coli_hip_set_fused_combine failed")
+
+
 ARM_AUTO, ARM_MFMA, ARM_GEMV = -1, 0, 2
 
 

@@ -304,6 +304,31 @@ def test_one_token_router_paths_match_oracle(hip, orc, fused, E, D, I, k, ga):
         hip.set_fused_route(-1)
 
 
+@pytest.mark.parametrize("fmt,gs", FORMATS)
+@pytest.mark.parametrize("ga", [0, 32])
+def test_one_token_fused_combine(hip, orc, fmt, gs, ga):
+    """One token: the down GEMV that also applies the router weights equals
+    the separate down + combine launches and the oracle bit for bit, for odd
+    and even k, a hidden size that is not a multiple of 16, and shapes past
+    its limits (k > 8, K > 1536: the separate launches then run)."""
+    say("fused combine", fmt, gs, ga)
+    rng = np.random.default_rng(1500 + fmt * 5 + gs + ga)
+    for E, D, I, k in ((9, 100, 96, 3), (20, 320, 192, 8), (18, 256, 4608, 16), (4, 64, 64, 1), (6, 96, 1536, 2),
+                       (10, 64, 1600, 4)):
+        gpu, ora, eset, x, logits = _layer_case(hip, orc, rng, E, D, I, 1, k, fmt=fmt, gs=gs or 32)
+        outs = []
+        for fc in (1, 0):
+            hip.set_fused_combine(fc)
+            try:
+                out, ids, w = _run_layer(hip, eset, x, logits, k, ga, 2)
+            finally:
+                hip.set_fused_combine(-1)
+            outs.append(out)
+        ref = orc.moe_forward(x, ids, w, ora, ga)
+        assert np.array_equal(outs[0], outs[1]), (E, D, I, k)
+        assert np.array_equal(outs[0], ref), (E, D, I, k, nerr(outs[0], ref))
+
+
 @pytest.mark.parametrize("ga", [0, 32])
 @pytest.mark.parametrize("arm", [2, 0])
 def test_moe_layer_matches_oracle(hip, orc, ga, arm):
