@@ -597,11 +597,14 @@ void launch_gemv_down_combine(const DotArgs &a, const MatGeom &g, int act, int k
 static int g_lds_limit = 64 * 1024;
 void set_lds_limit(int bytes) { g_lds_limit = bytes > 0 ? bytes : 64 * 1024; }
 
-// gate/up: 7 streaming waves + 1 chain wave (512 threads); down: 3 + 1.
-// Batches of 8 int4 blocks (4 int8 blocks): 4 KB of weights per wave in flight.
+// int4 gate/up: 11 streaming waves + 1 chain wave (768 threads), 5 blocks per
+// wave per round; int8 gate/up: 7 + 1 waves, 4 blocks; down: 3 + 1 waves, 8
+// int4 (4 int8) blocks. Measured on config 2, the int4 gate/up as 11 x 5
+// took 18.6 us against 19.3 us as 7 x 8 (about the same 55-56 blocks per
+// round); 13 x 4 and 15 x 4 were slower.
 template <bool W4, int EPI, bool GATEUP, int CH, bool ROUTE>
 static void launch_gemv_c(const DotArgs &a, const MatGeom &g, int grid_rows, hipStream_t st) {
-    constexpr int NW = GATEUP ? 7 : 3;
+    constexpr int NW = GATEUP ? (W4 ? 11 : 7) : 3;
     // the fused router keeps the expert descriptor table after the ring
     const size_t lds = gemv_ring_bytes<W4, NW, CH>() + (ROUTE ? (size_t)a.route.E * sizeof(ExpertDesc) : 0);
     auto kern = gemv_kernel<W4, EPI, GATEUP, NW, CH, ROUTE>;
@@ -613,17 +616,15 @@ static void launch_gemv_c(const DotArgs &a, const MatGeom &g, int grid_rows, hip
     hipLaunchKernelGGL(kern, grid, dim3((NW + 1) * 64), lds, st, a, g, a.xq, a.sx);
 }
 
-// gate/up: 7 streaming waves + 1 chain wave (512 threads); down: 3 + 1.
-// Batches of 8 int4 blocks (4 int8 blocks): 4 KB of weights per wave per round.
 template <bool W4, int EPI, bool GATEUP>
 static void launch_gemv_t(const DotArgs &a, const MatGeom &g, int grid_rows, hipStream_t st) {
     if constexpr (GATEUP) {
         if (a.route.logits) {
-            launch_gemv_c<W4, EPI, GATEUP, W4 ? 8 : 4, true>(a, g, grid_rows, st);
+            launch_gemv_c<W4, EPI, GATEUP, W4 ? 5 : 4, true>(a, g, grid_rows, st);
             return;
         }
     }
-    launch_gemv_c<W4, EPI, GATEUP, W4 ? 8 : 4, false>(a, g, grid_rows, st);
+    launch_gemv_c<W4, EPI, GATEUP, W4 ? (GATEUP ? 5 : 8) : 4, false>(a, g, grid_rows, st);
 }
 
 template <bool GATEUP>
