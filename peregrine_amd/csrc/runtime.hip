@@ -1144,7 +1144,10 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
     const int act = epi_act(ga);
     // one token routes to k distinct experts in top-k order, which is also
     // batch-union order: row r is (token 0, slot r) and no table is needed
-    const bool one_token = S == 1 && arm == COLI_HIP_ARM_GEMV;
+    // Ids from the router are always in range and distinct per token; ids
+    // from the caller may not be (out-of-range ids are skipped, repeats keep
+    // slot order), so those always go through the table.
+    const bool one_token = S == 1 && arm == COLI_HIP_ARM_GEMV && logits_dev;
     ExpertDesc *rdesc = nullptr;
     if (one_token && logits_dev) {
         if (!reserve(c, c->rdesc, (size_t)k * sizeof(ExpertDesc))) return 0;

@@ -579,6 +579,28 @@ def test_expert_table_duplicate_and_invalid_ids(hip, orc, S, k, E):
     assert np.array_equal(out, ref), nerr(out, ref)
 
 
+@pytest.mark.parametrize("arm", [2, -1, 0])
+def test_one_token_caller_ids(hip, orc, arm):
+    """One token with caller-supplied ids: out-of-range ids are skipped and a
+    repeated expert adds both rows in slot order, as in the oracle (these ids
+    go through the table, never straight to the expert descriptors)."""
+    say("one token caller ids", arm)
+    rng = np.random.default_rng(1700 + arm)
+    E, D, I, k = 10, 96, 64, 4
+    gpu, ora = _experts(rng, E, D, I, qt.FMT_I4G, 32, orc, hip)
+    eset = hip.ExpertSet(gpu)
+    x = rng.standard_normal((1, D)).astype(np.float32)
+    bx, bout = hip.DeviceBuffer.from_array(x), hip.DeviceBuffer(D * 4)
+    for ids in ([[3, -1, 3, 12]], [[0, 1, 2, 3]], [[-5, 10, 11, -1]], [[7, 7, 7, 7]]):
+        ids = np.array(ids, np.int32)
+        w = rng.random((1, k)).astype(np.float32)
+        bids, bw = hip.DeviceBuffer.from_array(ids), hip.DeviceBuffer.from_array(w)
+        hip.moe_forward_dev(eset, bx.ptr, 1, bids.ptr, bw.ptr, k, bout.ptr, 32, arm)
+        hip.pipe_sync(0)
+        ref = orc.moe_forward(x, ids, w, ora, 32)
+        np.testing.assert_array_equal(bout.download(np.float32, (1, D)), ref, err_msg=str(ids))
+
+
 @pytest.mark.parametrize("min_share,norm,scale", [(0.0, True, 2.5), (0.05, True, 1.0), (0.02, False, 1.7)])
 def test_sigmoid_router_matches_oracle(hip, orc, min_share, norm, scale):
     """The reference router (router.rs:52-170) on the device equals the
