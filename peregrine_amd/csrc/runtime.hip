@@ -185,13 +185,13 @@ int act_group() {
 }
 
 // Fused one-token router: -1 automatic, 0 never, 1 whenever eligible.
-// COLI_HIP_FUSED_ROUTE=0 in the environment turns the automatic choice off.
+// COLI_HIP_FUSED_ROUTE=0 (1) in the environment sets 0 (1) at first use.
 std::atomic<int> g_fused_route{-2};
 int fused_route_mode() {
     int m = g_fused_route.load();
     if (m == -2) {
         const char *e = getenv("COLI_HIP_FUSED_ROUTE");
-        m = e && e[0] == '0' ? 0 : -1;
+        m = e && e[0] == '0' ? 0 : (e && e[0] == '1' ? 1 : -1);
         g_fused_route.store(m);
     }
     return m;
