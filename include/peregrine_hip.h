@@ -131,8 +131,8 @@ int coli_hip_set_fused_route(int mode);
  * router weights in top-k order (one launch instead of down + combine; the
  * same bits). Eligible for k <= 8 and K <= 1536 (the down projection's input
  * width). -1 automatic (default: eligible and k <= 2), 0 never, 1 whenever
- * eligible. COLI_HIP_FUSED_COMBINE=0 in the environment turns the automatic
- * choice off. */
+ * eligible. COLI_HIP_FUSED_COMBINE=0 or =1 in the environment sets 0 or 1 at
+ * first use. */
 int coli_hip_set_fused_combine(int mode);
 
 /* ---- NEW: device-resident MoE layer (inputs already in HBM) ---- */

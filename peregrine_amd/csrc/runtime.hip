@@ -201,13 +201,13 @@ int fused_route_mode() {
 // more slots every weight block in flight at once streams slower than the
 // separate down GEMV's rounds: config 2, k = 8, 34.2 vs 32.5 us per layer;
 // config 1, k = 1, 15.2 vs 18.2 us), 0 never, 1 whenever eligible.
-// COLI_HIP_FUSED_COMBINE=0 in the environment sets 0 at first use.
+// COLI_HIP_FUSED_COMBINE=0 (1) in the environment sets 0 (1) at first use.
 std::atomic<int> g_fused_combine{-2};
 bool fused_combine_on(int k) {
     int m = g_fused_combine.load();
     if (m == -2) {
         const char *e = getenv("COLI_HIP_FUSED_COMBINE");
-        m = e && e[0] == '0' ? 0 : -1;
+        m = e && e[0] == '0' ? 0 : (e && e[0] == '1' ? 1 : -1);
         g_fused_combine.store(m);
     }
     return m == 1 || (m == -1 && k <= 2);
