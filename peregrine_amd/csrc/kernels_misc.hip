@@ -53,19 +53,11 @@ __global__ __launch_bounds__(1024) void quant_rows_kernel(QuantArgs a) {
 }
 
 __global__ __launch_bounds__(256) void quant_blocks_kernel(QuantArgs a) {
-    // ACT_B32: each 32-lane half-wave owns one 32-block; one load per thread.
-    const int row = blockIdx.y, tid = threadIdx.x;
-    const int b = blockIdx.x * 8 + (tid >> 5), l32 = tid & 31;
-    if (b * BLK >= a.Kp) return;
-    const float *x = a.x + (size_t)row * a.x_stride;
-    const int k = b * BLK + l32;
-    const float v = k < a.K ? x[k] : 0.0f;
-    const float m = warp_max(fabsf(v), 32);
-    float s = __fdiv_rn(m, 127.0f);
-    if (s < 1e-12f) s = 1e-12f;
-    const float inv = __fdiv_rn(1.0f, s);
-    a.q[(size_t)row * a.q_stride + perm8(k)] = (int8_t)(int)rintf(__fmul_rn(v, inv));
-    if (l32 == 0) a.s[(size_t)row * a.s_stride + b] = s;
+    // ACT_B32: 8 elements per thread, a workgroup covers 64 blocks of one row
+    const int row = blockIdx.y, nbk = a.Kp / BLK;
+    const int b_lo = blockIdx.x * 64, b_hi = min(nbk, b_lo + 64);
+    quant_row_b32(a.x + (size_t)row * a.x_stride, a.K, a.Kp, a.q + (size_t)row * a.q_stride,
+                  a.s + (size_t)row * a.s_stride, 4 * b_lo, 4 * b_hi, threadIdx.x, 256);
 }
 
 void launch_quant_rows(const QuantArgs &a, hipStream_t st) {
@@ -74,7 +66,7 @@ void launch_quant_rows(const QuantArgs &a, hipStream_t st) {
         hipLaunchKernelGGL(quant_rows_kernel, dim3(a.rows), dim3(1024), 0, st, a);
     } else {
         const int nb = a.Kp / BLK;
-        hipLaunchKernelGGL(quant_blocks_kernel, dim3((unsigned)((nb + 7) / 8), (unsigned)a.rows), dim3(256), 0, st,
+        hipLaunchKernelGGL(quant_blocks_kernel, dim3((unsigned)((nb + 63) / 64), (unsigned)a.rows), dim3(256), 0, st,
                            a);
     }
 }
@@ -366,36 +358,15 @@ __global__ __launch_bounds__(256) void route_quant_kernel(const float *logits, i
     const float *x = a.x + (size_t)s * a.x_stride;
     int8_t *q = a.q + (size_t)s * a.q_stride;
     if (a.mode == ACT_B32) {
-        // this slab's 32-blocks; 8 lanes per block, 4 elements per lane, a
-        // workgroup covers 32 blocks per step
+        // this slab's 32-blocks, 8 elements per thread; in the routing
+        // workgroup wave 0 routes while the other three quantise
         const int nbk = a.Kp / BLK;
         const int per = (nbk + (int)gridDim.y - 1) / (int)gridDim.y;
         const int b_lo = blockIdx.y * per, b_hi = min(nbk, b_lo + per);
-        const int sub = lane & 7;
-        for (int b = b_lo + wave * 8 + (lane >> 3); b - (wave * 8 + (lane >> 3)) < b_hi; b += 32) {
-            const bool ok = b < b_hi;   // the same for the 8 lanes of a block
-            float v[4];
-            float m = 0.0f;
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const int kx = b * BLK + sub * 4 + t;
-                v[t] = ok && kx < a.K ? x[kx] : 0.0f;
-                m = fmaxf(m, fabsf(v[t]));
-            }
-            m = fmaxf(m, __shfl_xor(m, 1));
-            m = fmaxf(m, __shfl_xor(m, 2));
-            m = fmaxf(m, __shfl_xor(m, 4));
-            float sc = __fdiv_rn(m, 127.0f);
-            if (sc < 1e-12f) sc = 1e-12f;
-            const float inv = __fdiv_rn(1.0f, sc);
-            if (ok) {
-#pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    const int kx = b * BLK + sub * 4 + t;
-                    q[perm8(kx)] = (int8_t)(int)rintf(__fmul_rn(v[t], inv));
-                }
-                if (sub == 0) a.s[(size_t)s * a.s_stride + b] = sc;
-            }
+        if (blockIdx.y == 0) {
+            if (wave > 0) quant_row_b32(x, a.K, a.Kp, q, a.s + (size_t)s * a.s_stride, 4 * b_lo, 4 * b_hi, tid - 64, 192);
+        } else {
+            quant_row_b32(x, a.K, a.Kp, q, a.s + (size_t)s * a.s_stride, 4 * b_lo, 4 * b_hi, tid, 256);
         }
         MISC_STAMP(blockIdx.y, 2);
     } else {

@@ -216,4 +216,30 @@ __device__ __forceinline__ float quant_group8(const float (&v)[8], float m_in, u
     return sc;
 }
 
+// ACT_B32 quantisation (quant.rs:14-33 per 32-block) of the 8-element groups
+// [g_lo, g_hi) of one row: thread t of nt cooperating threads takes groups
+// g_lo + t, g_lo + t + nt, ...; a 32-block is four consecutive threads, so
+// g_lo and nt are multiples of 4 and quads of threads are quad-aligned lanes.
+// Codes go out packed (8 bytes per group, device order), scales once per block.
+__device__ __forceinline__ void quant_row_b32(const float *x, int K, int Kp, int8_t *q, float *sc, int g_lo, int g_hi,
+                                              int t, int nt) {
+    const int ngr = Kp >> 3;
+    const bool vec = (K & 7) == 0 && ((uintptr_t)x & 15) == 0;
+    for (int base = g_lo; base < g_hi; base += nt) {
+        const int gi = base + t;
+        float v[8];
+        load_group8(x, gi < g_hi ? gi : ngr, K, vec, v);   // past the range: zeros
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) m = fmaxf(m, fabsf(v[j]));
+        m = quad_max(m);
+        uint2 pk;
+        const float s = quant_group8(v, m, pk);
+        if (gi < g_hi) {
+            *(uint2 *)(q + (size_t)gi * 8) = pk;
+            if ((gi & 3) == 0) sc[gi >> 2] = s;
+        }
+    }
+}
+
 }  // namespace phip
