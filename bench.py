@@ -104,6 +104,40 @@ def build_experts(hip, cfg, wfmt, seed):
     return layers
 
 
+def pcie_inclusive(hip, cfg, experts, bx, step_ids, step_w, step, ga, seconds=0.5):
+    """The reference's host-buffer entry point (coli_hip_expert_group_reduce,
+    lib.rs:620) on one step's routing: x rows and the layer output cross
+    PCIe on every call, which blocks. Reported beside the device-resident
+    rate, never as the benchmark value."""
+    S, D, k = cfg["S"], cfg["D"], cfg["k"]
+    x = bx.download(np.float32, ((step + 1) * S, D))[step * S:]
+    ids = step_ids.reshape(S, k)
+    w = step_w.reshape(S, k)
+    order, rows, xr, dst, rw = [], [], [], [], []
+    for e in dict.fromkeys(ids.reshape(-1).tolist()):   # batch-union order
+        toks = [t for t in range(S) for j in range(k) if ids[t, j] == e]
+        slots = [j for t in range(S) for j in range(k) if ids[t, j] == e]
+        order.append(e)
+        rows.append(len(toks))
+        for t, j in zip(toks, slots):
+            xr.append(x[t])
+            dst.append(t)
+            rw.append(w[t, j])
+    xr = np.stack(xr).astype(np.float32)
+    layout = hip.ReduceLayout.build(np.array(dst), S)
+    sel = [experts[e] for e in order]
+    hip.set_act_group(ga)
+    for _ in range(3):
+        hip.expert_group_reduce(sel, rows, xr, D, layout, np.array(rw, np.float32), S)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        hip.expert_group_reduce(sel, rows, xr, D, layout, np.array(rw, np.float32), S)
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    return {"tokens_per_s": round(S / dt, 1), "ms_per_call": round(dt * 1e3, 4), "calls": n,
+            "entry_point": "coli_hip_expert_group_reduce (host x in, host out; blocking)"}
+
+
 def make_logits(cfg, n_steps, seed):
     from peregrine_amd import synth
     rng = np.random.default_rng(seed)
@@ -339,6 +373,9 @@ def main():
             "setup_s": round(t_build, 1),
         },
     }
+    if S <= 64 and L == 1:
+        line["detail"]["pcie_inclusive"] = pcie_inclusive(hip, cfg, layers[0][1], bx, ids[0],
+                                                          bw.download(np.float32, (n_all, S * k))[warmup], warmup, ga)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg, args.wfmt, ga, args.cpu_seconds)
     else:
