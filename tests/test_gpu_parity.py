@@ -435,13 +435,14 @@ def test_batched_layer_full_width_sampled(hip, orc):
     assert nerr(out[sub], ref[sub]) <= TOL
 
 
-@pytest.mark.parametrize("S", [3, 1])
-def test_graph_replay_matches_eager(hip, orc, S):
-    """Replays of a captured layer equal eager runs (S = 1 exercises the
-    one-token path)."""
-    say("graph replay", S)
+@pytest.mark.parametrize("S,k,E", [(3, 2, 8), (1, 2, 8), (300, 8, 20)])
+def test_graph_replay_matches_eager(hip, orc, S, k, E):
+    """Replays of a captured layer equal eager runs, with eager work and
+    synchronisations between the replays (S = 1: the one-token path; S = 300,
+    k = 8: the three-launch expert table)."""
+    say("graph replay", S, k, E)
     rng = np.random.default_rng(91 + S)
-    E, D, I, k = 8, 256, 128, 2
+    D, I = 256, 128
     gpu, ora, eset, x, logits = _layer_case(hip, orc, rng, E, D, I, S, k)
     bx = hip.DeviceBuffer.from_array(x)
     bl = hip.DeviceBuffer.from_array(logits)
