@@ -370,9 +370,20 @@ __global__ __launch_bounds__(256) void mfma_dma_kernel(DotArgs a, MatGeom g) {
         if constexpr (EPI != EPI_ROW) lds_dma4(src_s + (size_t)grp_of(bc, g.gshift) * TILE_O, wv + ST::SW);
     };
 
-    // the tile's activation scales first (the compiler waits for these
-    // loads, and a wave's loads complete in order), then the first copies
-    if constexpr (EPI == EPI_B32) load_tile_sx(a, r0, rend, g.nb, sxl);
+    // the tile's activation scales ([nb][32] in LDS) by LDS-DMA, all issued
+    // at once: one copy per wave covers two blocks of the 32 rows. Nothing
+    // waits on them before block 0's wait, which covers them (a wave's loads
+    // complete in order). Rows past the tile's end repeat its last row.
+    if constexpr (EPI == EPI_B32) {
+        int rx = r0 + (lane & 31);
+        if (rx >= rend) rx = rend - 1;
+        const float *srcx = a.sx + (size_t)(a.act_identity ? rx : a.plan.row_act[rx]) * a.sx_stride;
+        const uint32_t sx_lds = lds_addr + (uint32_t)(NSTG * ST::BYTES);
+        for (int i = wave; i < (g.nb + 1) >> 1; i += 4) {
+            const int b = min(2 * i + (lane >> 5), g.nb - 1);
+            lds_dma4(srcx + b, sx_lds + (uint32_t)(i * 256));
+        }
+    }
 #pragma unroll
     for (int u = 0; u < PD; ++u)
         if (u < g.nb) copy_blk(u);
@@ -467,10 +478,9 @@ __global__ __launch_bounds__(256) void mfma_dma_kernel(DotArgs a, MatGeom g) {
                 } else {
                     wait_vm<0>();          // the last blocks: nothing copied past the end
                 }
-                // every wave's quarter of A (and, on the first pass, the
-                // activation scales) is in LDS once all waves are here
-                if (bb == 0) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // + sxl
-                else asm volatile("s_barrier" ::: "memory");
+                // every wave's quarter of A (and, on the first pass, its
+                // share of the activation scales) is in LDS once all waves are here
+                asm volatile("s_barrier" ::: "memory");
                 v4i A;
                 v4i B[NSUB];
                 read_ops(bb, A, B, Sr[u]);
@@ -555,7 +565,8 @@ static void launch_mfma_p(const DotArgs &a, const MatGeom &g, int grid_tiles, hi
 // stages plus (per-32 activation scales) the tile's scales
 template <bool W4, int EPI, int PD>
 static size_t mfma_dma_lds(const MatGeom &g) {
-    return (size_t)(PD + 2) * DmaStage<W4>::BYTES + (EPI == EPI_B32 ? (size_t)g.nb * 32 * sizeof(float) : 0);
+    // EPI_B32: the scales are copied two blocks at a time, so an odd nb rounds up
+    return (size_t)(PD + 2) * DmaStage<W4>::BYTES + (EPI == EPI_B32 ? (size_t)(g.nb + 1) / 2 * 2 * 32 * sizeof(float) : 0);
 }
 // Blocks in flight: three, when the stages and the tile's activation scales
 // fit three workgroups per CU (160 KB / 3); else two, if that fits three per
