@@ -231,6 +231,7 @@ struct DotArgs {   // shared by the GEMV and MFMA arms
     int act_zero;                                                       // activation row = 0 (one token)
     int n_rows_fixed;                                                   // >= 0: row count known on the host
     long long *trace;                                                   // optional phase timestamps (tests/tuning)
+    int w_reuse;                                                        // MFMA arm: M tiles re-read each expert's weights
     RouteArgs route;                                                    // gate/up GEMV: logits != null -> fused router
 };
 // grid_rows / grid_tiles: host-side upper bounds; the kernels read the true

@@ -274,15 +274,13 @@ __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const i
 }
 
 // ---------------------------------------------------------------------------
-// LDS-staged variant for weight-streaming shapes. Each wave copies its own
-// operands of a block (activations, weights, weight scales and, with 32-block
-// activation scales, those too) straight from HBM into a private LDS stage
-// with the LDS-DMA loads, PD blocks ahead, so the bytes in flight no longer
-// cost registers. A wave reads only what it copied itself: no barrier, just a
-// wait for its own older copies. The copies are issued from inline assembly
-// (the compiler would otherwise wait for every copy before any LDS read); the
-// loop issues no other vector-memory operation, so "older than the last
-// OPS*PD" is exactly the block about to be used.
+// LDS-staged variant (the default MFMA kernel). Operands travel from HBM
+// straight into shared LDS stages with the LDS-DMA loads, PD blocks ahead, so
+// the bytes in flight cost no registers. The copies are issued from inline
+// assembly (the compiler would otherwise wait for every copy before any LDS
+// read); the loop issues no other vector-memory operation, so "older than the
+// last OPS*PD" is exactly the block about to be used. Stage layout and the
+// per-block barrier: see DmaStage below.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void lds_dma16(const void *g, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory");
@@ -314,7 +312,7 @@ struct DmaStage {
     static constexpr int BYTES = WAVE0 + 4 * WAVE_BYTES;
 };
 
-template <bool W4, int EPI, bool GATEUP, int NSUB, int PD>
+template <bool W4, int EPI, bool GATEUP, int NSUB, int PD, bool WNT>
 __global__ __launch_bounds__(256) void mfma_dma_kernel(DotArgs a, MatGeom g) {
     static_assert(NSUB == 2, "a wave's weight copy covers two 32-column subtiles");
     typedef DmaStage<W4> ST;
@@ -361,11 +359,17 @@ __global__ __launch_bounds__(256) void mfma_dma_kernel(DotArgs a, MatGeom g) {
         const uint32_t st = lds_addr + (uint32_t)((b % NSTG) * ST::BYTES);
         const uint32_t wv = st + ST::WAVE0 + wave * ST::WAVE_BYTES;
         lds_dma4(src_a + (size_t)bc * BLK, st + ST::A + wave * 256);
+        // weights read once per dispatch stream past the caches (WNT); weights
+        // that several M tiles of an expert re-read are left cacheable
+        auto wcopy = [&](const void *src, uint32_t dst) {
+            if constexpr (WNT) lds_dma16_nt(src, dst);
+            else lds_dma16(src, dst);
+        };
         if constexpr (W4) {
-            lds_dma16_nt(src_w + (size_t)bc * TILE_O * BB, wv);
+            wcopy(src_w + (size_t)bc * TILE_O * BB, wv);
         } else {
-            lds_dma16_nt(src_w8[0] + (size_t)bc * TILE_O * BB, wv);
-            lds_dma16_nt(src_w8[1] + (size_t)bc * TILE_O * BB, wv + 1024);
+            wcopy(src_w8[0] + (size_t)bc * TILE_O * BB, wv);
+            wcopy(src_w8[1] + (size_t)bc * TILE_O * BB, wv + 1024);
         }
         if constexpr (EPI != EPI_ROW) lds_dma4(src_s + (size_t)grp_of(bc, g.gshift) * TILE_O, wv + ST::SW);
     };
@@ -576,19 +580,29 @@ static size_t mfma_dma_lds(const MatGeom &g) {
 // two per CU).
 constexpr int DMA_PD_SHALLOW = 3, DMA_PD_NARROW = 2, DMA_PD_DEEP_W4 = 6, DMA_PD_W8 = 3;
 
-template <bool W4, int EPI, bool GATEUP, int PD>
-static void launch_mfma_dma(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
+template <bool W4, int EPI, bool GATEUP, int PD, bool WNT>
+static void launch_mfma_dma_h(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
     constexpr int NSUB = 2;
     const int ch_per_wg = GATEUP ? 4 * 32 : 4 * 32 * NSUB;
     const int span = GATEUP ? ((g.O + 31) & ~31) : g.O;
     dim3 grid((unsigned)((span + ch_per_wg - 1) / ch_per_wg), (unsigned)grid_tiles);
     const size_t lds = mfma_dma_lds<W4, EPI, PD>(g);
-    auto kern = mfma_dma_kernel<W4, EPI, GATEUP, NSUB, PD>;
+    auto kern = mfma_dma_kernel<W4, EPI, GATEUP, NSUB, PD, WNT>;
     static size_t attr_set = 64 * 1024;
     if (lds > attr_set &&
         hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess)
         attr_set = lds;
     hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, a, g);
+}
+
+// Weights are copied non-temporally unless the dispatch re-reads them (about
+// two or more M tiles per expert on average). Measured: config 4 (102 rows
+// per expert) 1.85 -> 1.72 ms cacheable; configs 3 and 5 (3 and 16 rows)
+// 4-7% slower cacheable.
+template <bool W4, int EPI, bool GATEUP, int PD>
+static void launch_mfma_dma(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
+    if (a.w_reuse) launch_mfma_dma_h<W4, EPI, GATEUP, PD, false>(a, g, grid_tiles, st);
+    else launch_mfma_dma_h<W4, EPI, GATEUP, PD, true>(a, g, grid_tiles, st);
 }
 
 // COLI_HIP_MFMA_DMA: -1 (default) the LDS-staged kernel wherever its stages

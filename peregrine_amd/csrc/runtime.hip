@@ -486,6 +486,7 @@ struct DispatchOpts {
     bool act_zero = false;      // every row reads activation row 0 (one token)
     int n_rows_fixed = -1;      // row count known on the host
     RouteArgs route{};          // one token: router + quant fused into the gate/up GEMV
+    int w_reuse = 0;                    // about two or more M tiles per expert: weights stay cacheable
     const float *combine_w = nullptr;   // one token: down + combine in one launch, weights [k]
     float *combine_out = nullptr;       //   and the layer output [D]
 };
@@ -521,6 +522,7 @@ void run_experts(Ctx *c, Prof &prof, const ExpertDesc *desc, const RowPlan &plan
     da.act_zero = opt.act_zero ? 1 : 0;
     da.n_rows_fixed = opt.n_rows_fixed;
     da.route = opt.route;
+    da.w_reuse = opt.w_reuse;
     prof.mark(COLI_HIP_K_GATEUP);
     if (arm == COLI_HIP_ARM_GEMV)
         launch_gemv_gateup(da, gg, act, R_bound, c->stream);
@@ -663,6 +665,7 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
     plan.mt_rend = di + total + 2 * T;
     plan.counts = di + total + 3 * T;
     DispatchOpts opt;
+    opt.w_reuse = total >= 2 * MT_ROWS * count;   // about two or more M tiles per expert
     run_experts(c, prof, (const ExpertDesc *)dm, plan, gg, gd, x_dev, total, true, total, T, ga, arm, s, opt);
     float *res = s.y;
     if (red) {
@@ -1141,6 +1144,7 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
 
     Prof prof(c);
     DispatchOpts opt;
+    opt.w_reuse = R >= 2 * MT_ROWS * E;   // about two or more M tiles per expert
     const int act = epi_act(ga);
     // one token routes to k distinct experts in top-k order, which is also
     // batch-union order: row r is (token 0, slot r) and no table is needed
