@@ -53,6 +53,8 @@ def parse():
     ap.add_argument("--arm", choices=("auto", "gemv", "mfma"), default="auto")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-pcie", action="store_true",
+                    help="skip the host-buffer (PCIe-inclusive) timing, e.g. under a profiler")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--experts", type=int, default=None, help="override the resident expert count (experiments)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -373,7 +375,7 @@ def main():
             "setup_s": round(t_build, 1),
         },
     }
-    if S <= 64 and L == 1:
+    if S <= 64 and L == 1 and not args.no_pcie:
         line["detail"]["pcie_inclusive"] = pcie_inclusive(hip, cfg, layers[0][1], bx, ids[0],
                                                           bw.download(np.float32, (n_all, S * k))[warmup], warmup, ga)
     if not args.no_cpu_baseline:
