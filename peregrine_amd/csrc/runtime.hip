@@ -550,9 +550,6 @@ void run_experts(Ctx *c, Prof &prof, const ExpertDesc *desc, const RowPlan &plan
     dd.act_zero = 0;
     dd.route = RouteArgs{};
     prof.mark(COLI_HIP_K_DOWN);
-#ifdef PHIP_STAGE_EXP
-    if (getenv("PHIP_STAGES") && atoi(getenv("PHIP_STAGES")) < 2) return;
-#endif
     if (arm == COLI_HIP_ARM_GEMV && opt.combine_out) {
         launch_gemv_down_combine(dd, gd, act, opt.n_rows_fixed, opt.combine_w, opt.combine_out, c->stream);
     } else if (arm == COLI_HIP_ARM_GEMV) {
@@ -1199,9 +1196,6 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
     }
     run_experts(c, prof, set->desc_dev, plan, gg, gd, x_dev, S, false, R, tmax, ga, arm, s, opt);
     prof.mark(COLI_HIP_K_COMBINE);
-#ifdef PHIP_STAGE_EXP
-    if (getenv("PHIP_STAGES") && atoi(getenv("PHIP_STAGES")) < 3) { prof.mark(-1); prof.finish(); return 1; }
-#endif
     if (fuse_dc) {
         // combined by the down GEMV
     } else if (one_token) {   // rows 0..k-1 of token 0, in top-k order
