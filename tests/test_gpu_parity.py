@@ -373,11 +373,12 @@ def test_moe_layer_fused_router_matches_oracle(hip, orc, S, arm, ga):
 @pytest.mark.parametrize("ga", [32, 0])
 @pytest.mark.parametrize("fmt,gs", FORMATS)
 def test_mfma_dense_and_streaming_dispatches(hip, orc, ga, fmt, gs):
-    """MFMA dispatches with many rows per expert (full 32-row tiles) and with
-    under two (ragged tiles) equal the oracle bit for bit."""
+    """MFMA dispatches with many rows per expert (full 32-row tiles; two or
+    more tiles per expert, so the weight copies stay cacheable) and with
+    under two (ragged tiles, non-temporal copies) equal the oracle bit for bit."""
     say("mfma dense/streaming", ga, fmt, gs)
     rng = np.random.default_rng(610 + ga + fmt)
-    for E, S, k in ((3, 64, 2), (16, 9, 3)):   # 43 rows per expert, then under 2
+    for E, S, k in ((3, 100, 2), (16, 9, 3)):   # 67 rows per expert, then under 2
         gpu, ora, eset, x, logits = _layer_case(hip, orc, rng, E, 288, 160, S, k, fmt=fmt, gs=gs or 32)
         out, ids, w = _run_layer(hip, eset, x, logits, k, ga, 2)
         ref = orc.moe_forward(x, ids, w, ora, ga)
@@ -431,6 +432,20 @@ def test_batched_layer_full_width_sampled(hip, orc):
     gpu, ora, eset, x, logits = _layer_case(hip, orc, rng, E, D, I, S, k, zipf=True)
     out, ids, w = _run_layer(hip, eset, x, logits, k, 32, -1)
     sub = np.array([0, 5, 17, 33, 48, 63])
+    ref = orc.moe_forward(x, ids, w, ora, 32, subset=sub, nthreads=8)
+    assert nerr(out[sub], ref[sub]) <= TOL
+
+
+def test_prefill_layer_full_width_sampled(hip, orc):
+    """BASELINE config 4 widths (2048 tokens, Zipf top-8; about 680 rows per
+    expert, so every expert spans many M tiles and the weight copies stay
+    cacheable), checked on 6 sampled tokens."""
+    say("prefill 2048 tokens")
+    rng = np.random.default_rng(2048)
+    E, D, I, S, k = 24, 5120, 1536, 2048, 8
+    gpu, ora, eset, x, logits = _layer_case(hip, orc, rng, E, D, I, S, k, zipf=True)
+    out, ids, w = _run_layer(hip, eset, x, logits, k, 32, -1)
+    sub = np.array([0, 1, 511, 1024, 1777, 2047])
     ref = orc.moe_forward(x, ids, w, ora, 32, subset=sub, nthreads=8)
     assert nerr(out[sub], ref[sub]) <= TOL
 
