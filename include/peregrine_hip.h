@@ -92,6 +92,9 @@ int coli_hip_expert_group_reduce(ColiHipTensor *const *gates, ColiHipTensor *con
 /* ---- graphs: replaces backend_cuda.h:172-190 ---- */
 int coli_hip_graph_begin(int device);                             /* coli_cuda_graph_begin */
 int coli_hip_graph_end(int device, ColiHipGraph **out);           /* coli_cuda_graph_end */
+/* graph_launch refuses (returns 0) a graph captured before the device's
+ * scratch buffers were reallocated by a larger call; scratch never grows
+ * during a capture (run each call shape eagerly once before capturing it). */
 int coli_hip_graph_launch(ColiHipGraph *g);                       /* coli_cuda_graph_launch */
 void coli_hip_graph_free(ColiHipGraph *g);                        /* coli_cuda_graph_free */
 void coli_hip_graph_cache_stats(uint64_t *captures, uint64_t *replays, uint64_t *invalidations,

@@ -11,6 +11,18 @@
 
 namespace phip {
 
+// Dynamic LDS above 64 KB needs an explicit opt-in, per kernel and per
+// device. `opted` is the caller's per-kernel table, indexed by device.
+constexpr int LDS_OPT_DEVICES = 64;
+inline void lds_opt_in(const void *kern, size_t lds, size_t (&opted)[LDS_OPT_DEVICES]) {
+    if (lds <= 64 * 1024) return;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= LDS_OPT_DEVICES) return;
+    if (lds > opted[dev] &&
+        hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess)
+        opted[dev] = lds;
+}
+
 // ---- activation scale granularity ("act group") ----
 // ACT_ROW: one scale per row (qrow_i8, peregrine-kernels/src/quant.rs:14-33).
 // ACT_B32: one scale per 32-element block (BASELINE extension).

@@ -594,10 +594,8 @@ static void launch_gemv_c(const DotArgs &a, const MatGeom &g, int grid_rows, hip
     // the fused router keeps the expert descriptor table after the ring
     const size_t lds = gemv_ring_bytes<W4, NW, CH>() + (ROUTE ? (size_t)a.route.E * sizeof(ExpertDesc) : 0);
     auto kern = gemv_kernel<W4, EPI, GATEUP, NW, CH, ROUTE>;
-    static size_t attr_set = 64 * 1024;   // dynamic LDS above 64 KB needs an explicit opt-in
-    if (lds > attr_set &&
-        hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess)
-        attr_set = lds;
+    static size_t opted[LDS_OPT_DEVICES];
+    lds_opt_in((const void *)kern, lds, opted);
     dim3 grid(GATEUP ? (unsigned)((g.O + 31) / 32) : (unsigned)((g.O + 63) / 64), (unsigned)grid_rows);
     hipLaunchKernelGGL(kern, grid, dim3((NW + 1) * 64), lds, st, a, g, a.xq, a.sx);
 }

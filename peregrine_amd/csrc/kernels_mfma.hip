@@ -588,10 +588,8 @@ static void launch_mfma_dma_h(const DotArgs &a, const MatGeom &g, int grid_tiles
     dim3 grid((unsigned)((span + ch_per_wg - 1) / ch_per_wg), (unsigned)grid_tiles);
     const size_t lds = mfma_dma_lds<W4, EPI, PD>(g);
     auto kern = mfma_dma_kernel<W4, EPI, GATEUP, NSUB, PD, WNT>;
-    static size_t attr_set = 64 * 1024;
-    if (lds > attr_set &&
-        hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess)
-        attr_set = lds;
+    static size_t opted[LDS_OPT_DEVICES];
+    lds_opt_in((const void *)kern, lds, opted);
     hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, a, g);
 }
 

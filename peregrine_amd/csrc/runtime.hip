@@ -36,6 +36,7 @@ struct ColiHipGraph {
     hipGraph_t graph;
     hipGraphExec_t exec;
     int device;
+    unsigned gen;   // the device's scratch generation at capture: the graph holds those buffers' addresses
 };
 
 struct ColiHipExpertSet {
@@ -244,9 +245,16 @@ int select_ctx(Ctx *c) {
 
 // Grow-only device scratch. A reallocation bumps the generation so anything
 // holding baked addresses (captured graphs) knows it is stale.
+// Scratch must not move while a capture is recording addresses into it.
+static int capturing(Ctx *c) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(c->stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+
 int reserve(Ctx *c, Buf &b, size_t bytes) {
     if (bytes == 0) bytes = 256;
     if (b.cap >= bytes) return 1;
+    if (capturing(c)) return fail("scratch would grow during graph capture: run the same call eagerly first");
     if (b.p) hipFree(b.p);
     b.p = nullptr;
     b.cap = 0;
@@ -259,6 +267,7 @@ int reserve(Ctx *c, Buf &b, size_t bytes) {
 int reserve_pinned(Ctx *c, Buf &b, size_t bytes) {
     if (bytes == 0) bytes = 256;
     if (b.cap >= bytes) return 1;
+    if (capturing(c)) return fail("staging would grow during graph capture: run the same call eagerly first");
     if (b.p) hipHostFree(b.p);
     b.p = nullptr;
     b.cap = 0;
@@ -871,6 +880,7 @@ int coli_hip_graph_end(int device, ColiHipGraph **out) {
     g->graph = graph;
     g->exec = exec;
     g->device = device;
+    g->gen = c->gen;
     *out = g;
     return 1;
 }
@@ -879,6 +889,7 @@ int coli_hip_graph_launch(ColiHipGraph *g) {
     if (!g) return 0;
     Ctx *c = find_ctx(g->device);
     if (!select_ctx(c)) return 0;
+    if (c->gen != g->gen) return fail("graph launch: scratch was reallocated after the capture; capture the graph again");
     if (!hip_ok(hipGraphLaunch(g->exec, c->stream), "graph launch")) return 0;
     return hip_ok(hipStreamSynchronize(c->stream), "graph synchronize");
 }

@@ -484,6 +484,38 @@ def test_graph_replay_matches_eager(hip, orc, S, k, E):
     assert np.array_equal(bout.download(np.float32, (S, D)), eager)
 
 
+def test_graph_refused_after_scratch_growth(hip, orc):
+    """A captured layer holds the addresses of the library's scratch buffers.
+    Once a larger eager call reallocates them, launching the old graph is
+    refused on the host (nothing runs), and a fresh capture replays the
+    eager result."""
+    say("graph refused after scratch growth")
+    rng = np.random.default_rng(4321)
+    E, D, I, S, k = 8, 256, 128, 3, 2
+    gpu, ora, eset, x, logits = _layer_case(hip, orc, rng, E, D, I, S, k)
+    bx, bl = hip.DeviceBuffer.from_array(x), hip.DeviceBuffer.from_array(logits)
+    bids, bw, bout = hip.DeviceBuffer(S * k * 4), hip.DeviceBuffer(S * k * 4), hip.DeviceBuffer(S * D * 4)
+
+    def body():
+        hip.route_softmax_topk_dev(0, bl.ptr, S, E, k, bids.ptr, bw.ptr)
+        hip.moe_forward_dev(eset, bx.ptr, S, bids.ptr, bw.ptr, k, bout.ptr, 32, -1)
+
+    body()
+    hip.pipe_sync(0)
+    eager = bout.download(np.float32, (S, D))
+    g = hip.capture(0, body)
+    g.launch()
+    assert np.array_equal(bout.download(np.float32, (S, D)), eager)
+    # 65536 rows: more than any other call in the suite, so the row tables grow
+    big_x = rng.standard_normal((8192, D)).astype(np.float32)
+    _run_layer(hip, eset, big_x, synth.normal_logits(rng, 8192, E), 8, 32, -1)
+    with pytest.raises(hip.HipError):
+        g.launch()
+    g2 = hip.capture(0, body)
+    g2.launch()
+    assert np.array_equal(bout.download(np.float32, (S, D)), eager)
+
+
 def test_greedy_argmax_token_identical(hip, orc):
     """Random-init MoE-only stack (embedding -> 3 MoE layers with residual ->
     lm_head argmax); the GPU and the oracle generate the same tokens."""
