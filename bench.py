@@ -235,6 +235,8 @@ def main():
     if args.experts:
         cfg["E"] = args.experts
         cfg["name"] += f"_E{args.experts}"
+    if args.wfmt == "int8":
+        cfg["name"] += "_int8"
     steps = args.steps if args.steps is not None else {1: 200, 2: 200, 3: 100, 4: 20, 5: 10}[args.config]
     warmup = args.warmup if args.warmup is not None else max(2, steps // 10)
     from peregrine_amd import hip
