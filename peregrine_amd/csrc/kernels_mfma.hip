@@ -316,7 +316,8 @@ struct DmaStage {
 // SIMD (its stages and activation scales fit four workgroups per CU up to
 // K = 2048). Measured: config 4 down 527 -> 497 us; configs 3 and 5 flat. The
 // gate/up kernels (138 VGPRs, LDS for three workgroups per CU) and the int8
-// down projection (which would spill more) are left uncapped.
+// down projection are left uncapped (capped, it spills eight registers:
+// config 5 int8 down 735 vs 630 us).
 template <bool W4, int EPI, bool GATEUP, int NSUB, int PD, bool WNT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATEUP || !W4 ? 1 : 4))) void mfma_dma_kernel(DotArgs a, MatGeom g) {
     static_assert(NSUB == 2, "a wave's weight copy covers two 32-column subtiles");
