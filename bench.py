@@ -1,25 +1,30 @@
 """Benchmark of the MI355X MoE expert lane on BASELINE.json's configurations.
 
-A step is one routed MoE layer over one batch of synthetic tokens: device
-router (softmax top-k) -> expert-offset table -> int8 activation quant ->
-fused gate/up + SwiGLU (+ h quant) -> down -> weighted combine. Inputs
-(tokens, router logits, 160+ resident experts) are in HBM before timing
-starts; every step uses its own tokens and router logits, so the experts a
-step reads change from step to step.
+A step is one routed MoE layer (config 5: four resident layers back to back)
+over one batch of synthetic tokens: device router (softmax top-k) ->
+expert-offset table -> int8 activation quant -> fused gate/up + SwiGLU (+ h
+quant) -> down -> weighted combine. Inputs (tokens, router logits, resident
+experts) are in HBM before timing starts; every step uses its own tokens and
+router logits, so the experts a step reads change from step to step.
 
-    python bench.py                      # config 2 (decode, batch 1), 1 GPU
-    python bench.py --config 4           # prefill, 2048 tokens
+    python bench.py                      # config 5 (the largest single-GPU one), int4
+    python bench.py --config 2           # decode, batch 1 (headline = that config)
     python bench.py --config 5 --wfmt int8
 
-Prints one JSON line (the driver's contract). Per-kernel durations come from
-HIP events recorded on the library's device stream in a second, profiled
-pass over the same steps.
+The JSON line's headline is the chosen config. Unless --no-detail, it also
+carries the decode config 2 (HBM fraction) and the prefill config 4 (int8
+MFMA fraction) under detail.workloads, each with its own roofline.
+
+Kernel durations come from HIP events that the kernels' own dispatch packets
+record (hipExtLaunchKernelGGL) in a second, profiled pass over the same steps:
+kernel execution alone, as rocprofv3's kernel trace measures it.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import platform
 import sys
 import time
 
@@ -39,6 +44,7 @@ CONFIGS = {
     4: dict(name="cfg4_prefill_2048tok_zipf", E=160, D=5120, I=1536, S=2048, k=8, route="zipf", layers=1),
     5: dict(name="cfg5_large_layer_512tok_256x", E=256, D=6144, I=2048, S=512, k=8, route="normal", layers=4),
 }
+DEFAULT_STEPS = {1: 200, 2: 200, 3: 100, 4: 20, 5: 20}
 
 
 def parse():
@@ -46,16 +52,18 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
+    ap.add_argument("--config", type=int, default=5, choices=sorted(CONFIGS))
     ap.add_argument("--wfmt", choices=("int4", "int8"), default="int4")
     ap.add_argument("--act-group", type=int, default=32, choices=(0, 32),
                     help="activation scale per 32-block (BASELINE, default) or per row (reference)")
     ap.add_argument("--arm", choices=("auto", "gemv", "mfma"), default="auto")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
+    ap.add_argument("--no-detail", action="store_true", help="only the chosen config (no config 2 / 4 lines)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-pcie", action="store_true",
                     help="skip the host-buffer (PCIe-inclusive) timing, e.g. under a profiler")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+                    help="CPU work per thread setting of the baseline (single thread, then all cores)")
     ap.add_argument("--experts", type=int, default=None, help="override the resident expert count (experiments)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device-to-device copy kernel 5 times (scales rocprofv3 "
@@ -106,38 +114,46 @@ def build_experts(hip, cfg, wfmt, seed):
     return layers
 
 
-def pcie_inclusive(hip, cfg, experts, bx, step_ids, step_w, step, ga, seconds=0.5):
+def pcie_inclusive(hip, cfg, experts, x_step, ids, w, ga, seconds=0.5):
     """The reference's host-buffer entry point (coli_hip_expert_group_reduce,
     lib.rs:620) on one step's routing: x rows and the layer output cross
-    PCIe on every call, which blocks. Reported beside the device-resident
-    rate, never as the benchmark value."""
+    PCIe on every call, which blocks. Timed eagerly and with the automatic
+    graph cache (COLI_HIP_GRAPH=1). Reported beside the device-resident rate,
+    never as the benchmark value."""
     S, D, k = cfg["S"], cfg["D"], cfg["k"]
-    x = bx.download(np.float32, ((step + 1) * S, D))[step * S:]
-    ids = step_ids.reshape(S, k)
-    w = step_w.reshape(S, k)
+    ids = ids.reshape(S, k)
+    w = w.reshape(S, k)
     order, rows, xr, dst, rw = [], [], [], [], []
     for e in dict.fromkeys(ids.reshape(-1).tolist()):   # batch-union order
-        toks = [t for t in range(S) for j in range(k) if ids[t, j] == e]
-        slots = [j for t in range(S) for j in range(k) if ids[t, j] == e]
+        for t in range(S):
+            for j in range(k):
+                if ids[t, j] == e:
+                    xr.append(x_step[t])
+                    dst.append(t)
+                    rw.append(w[t, j])
         order.append(e)
-        rows.append(len(toks))
-        for t, j in zip(toks, slots):
-            xr.append(x[t])
-            dst.append(t)
-            rw.append(w[t, j])
+        rows.append(int(np.sum(ids == e)))
     xr = np.stack(xr).astype(np.float32)
+    rw = np.array(rw, np.float32)
     layout = hip.ReduceLayout.build(np.array(dst), S)
     sel = [experts[e] for e in order]
     hip.set_act_group(ga)
-    for _ in range(3):
-        hip.expert_group_reduce(sel, rows, xr, D, layout, np.array(rw, np.float32), S)
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        hip.expert_group_reduce(sel, rows, xr, D, layout, np.array(rw, np.float32), S)
-        n += 1
-    dt = (time.perf_counter() - t0) / n
-    return {"tokens_per_s": round(S / dt, 1), "ms_per_call": round(dt * 1e3, 4), "calls": n,
-            "entry_point": "coli_hip_expert_group_reduce (host x in, host out; blocking)"}
+    out = {}
+    for mode in ("eager", "graph_cache"):
+        os.environ["COLI_HIP_GRAPH"] = "1" if mode == "graph_cache" else "0"
+        try:
+            for _ in range(3):
+                hip.expert_group_reduce(sel, rows, xr, D, layout, rw, S)
+            n, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < seconds:
+                hip.expert_group_reduce(sel, rows, xr, D, layout, rw, S)
+                n += 1
+            dt = (time.perf_counter() - t0) / n
+        finally:
+            os.environ.pop("COLI_HIP_GRAPH", None)
+        out[mode] = {"tokens_per_s": round(S / dt, 1), "ms_per_call": round(dt * 1e3, 4), "calls": n}
+    out["entry_point"] = "coli_hip_expert_group_reduce (host x in, host out; blocking; Python ctypes call included)"
+    return out
 
 
 def make_logits(cfg, n_steps, seed):
@@ -153,36 +169,69 @@ def make_logits(cfg, n_steps, seed):
     return out
 
 
+def cpu_info():
+    model = platform.processor() or "unknown"
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return model, os.cpu_count() or 1
+
+
+def cpu_threads():
+    """All cores this process may use: the affinity set, capped by the
+    OMP_NUM_THREADS-style share the GPU box gives one GPU."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    cap = os.environ.get("OMP_NUM_THREADS")
+    if cap and cap.isdigit() and int(cap) > 0:
+        n = min(n, int(cap))
+    return max(n, 1)
+
+
 def cpu_baseline(cfg, wfmt, ga, seconds):
     """The oracle's AVX2 restatement of the reference CPU path (dot_i4i8_avx2,
-    idot.rs:214-239) over one layer: tokens one at a time, experts in parallel
-    over threads (par_map, mlp.rs:96-104). Timed on this host for a bounded
-    sample of tokens."""
+    idot.rs:214-239; the expert is Mlp::swiglu, mlp.rs:21-26, the combine the
+    moe_forward scatter, mlp.rs:111-119) over a bounded sample of the
+    workload's tokens, single-threaded and on all cores (threads over the
+    routed experts, as par_map in mlp.rs:96-104). The sample's expert slots
+    alias 16 distinct host experts of the configuration's shape (host memory
+    and set-up time); each expert is still streamed from DRAM per use."""
     from oracle import oracle as orc
     from peregrine_amd import qt, synth
-    D, I = cfg["D"], cfg["I"]
-    E = min(cfg["E"], 16)
-    k = min(cfg["k"], E)
+    D, I, E, k = cfg["D"], cfg["I"], cfg["E"], cfg["k"]
     rng = np.random.default_rng(99)
     fmt = qt.FMT_I4G if wfmt == "int4" else qt.FMT_I8G
-    experts = []
-    for _ in range(E):
+    n_dist = min(E, 16)
+    dist = []
+    for _ in range(n_dist):
         trip = synth.make_expert(rng, D, I, fmt, 32)
         shp = ((I, D), (I, D), (D, I))
-        experts.append(tuple(orc.Tensor(t[0], t[1], fmt, i, o, 32) for t, (o, i) in zip(trip, shp)))
-    threads = min(os.cpu_count() or 1, 16, max(k, 1))
-    n, t0 = 0, time.perf_counter()
-    while True:
-        x = rng.standard_normal((1, D)).astype(np.float32)
-        idx, w = orc.route_softmax_topk(synth.normal_logits(rng, 1, E), k)
-        orc.moe_forward(x, idx, w, experts, ga, nthreads=threads, simd=orc.have_avx2())
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or n >= 2000:
-            break
-    return dict(value=round(n / el, 3), unit="tokens/s", cores=threads, kind="port",
-                sample=f"{n} single-token MoE-layer forwards (top-{k} of {E} experts, D={D}, I={I}, "
-                       f"{wfmt} gs=32, act group {ga}), AVX2 int4 dot, {threads} threads over experts")
+        dist.append(tuple(orc.Tensor(t[0], t[1], fmt, i, o, 32) for t, (o, i) in zip(trip, shp)))
+    experts = [dist[e % n_dist] for e in range(E)]
+    S = min(cfg["S"], 16)
+    model, nproc = cpu_info()
+    res = {}
+    for label, threads in (("single", 1), ("all", cpu_threads())):
+        n, t0 = 0, time.perf_counter()
+        while True:
+            x = rng.standard_normal((S, D)).astype(np.float32)
+            logits = synth.zipf_logits(rng, S, E) if cfg["route"] == "zipf" else synth.normal_logits(rng, S, E)
+            idx, w = orc.route_softmax_topk(logits, k)
+            orc.moe_forward(x, idx, w, experts, ga, nthreads=threads, simd=orc.have_avx2())
+            n += S
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                break
+        res[label] = (n / el, threads, n)
+    return dict(value=round(res["all"][0], 3), unit="tokens/s", cores=res["all"][1], kind="port",
+                single_thread_value=round(res["single"][0], 3), nproc=nproc, cpu_model=model,
+                sample=f"{res['single'][2]} tokens single-threaded and {res['all'][2]} on {res['all'][1]} threads, "
+                       f"in batches of {S} tokens of {cfg['name']} (top-{k} of {E} expert slots aliasing "
+                       f"{n_dist} distinct experts, D={D}, I={I}, {wfmt} gs=32, act group {ga}); AVX2 "
+                       f"restatement of dot_i4i8_avx2, threads over routed experts")
 
 
 METRIC = "MoE-layer tokens/s + HBM GB/s % peak (decode) / int8 MFMA % peak (prefill)"
@@ -222,33 +271,16 @@ def measured_traffic(workload):
     return None
 
 
-def main():
-    args = parse()
-    if args.calibrate_copy:
-        calibrate_copy()
-        return
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1 "
-                                   "(no collectives or sharding in scope)"}))
-        sys.exit(2)
-    cfg = dict(CONFIGS[args.config])
-    if args.experts:
-        cfg["E"] = args.experts
-        cfg["name"] += f"_E{args.experts}"
-    if args.wfmt == "int8":
-        cfg["name"] += "_int8"
-    steps = args.steps if args.steps is not None else {1: 200, 2: 200, 3: 100, 4: 20, 5: 10}[args.config]
-    warmup = args.warmup if args.warmup is not None else max(2, steps // 10)
-    from peregrine_amd import hip
-
-    assert hip.init([0]) == 1, "coli_hip_init failed"
+def run_workload(hip, cfg, wfmt, ga, arm, steps, warmup, use_graph=True, layers=None, pcie=False):
+    """Times `steps` steps of one workload (after `warmup` eager ones), then
+    a profiled pass over the same steps for per-kernel durations. Returns
+    (summary dict, layers) so a later workload of the same shape can reuse
+    the resident experts."""
     S, D, E, k, L = cfg["S"], cfg["D"], cfg["E"], cfg["k"], cfg["layers"]
-    arm = {"auto": -1, "gemv": hip.ARM_GEMV, "mfma": hip.ARM_MFMA}[args.arm]
-    ga = args.act_group
     t_build = time.perf_counter()
-    layers = build_experts(hip, cfg, args.wfmt, seed=args.config)
+    if layers is None:
+        layers = build_experts(hip, cfg, wfmt, seed=cfg.get("seed", 1))
     n_all = warmup + steps
-    # inputs for every step resident in HBM
     bx = hip.DeviceBuffer(n_all * S * D * 4)
     bx.fill(n_all * S * D, 1, 0.0, 1.0, seed=7)
     logits = make_logits(cfg, n_all, seed=11)
@@ -273,12 +305,10 @@ def main():
                 hip.moe_forward_dev(layers[layer][0], cur, S, ip, wp, k, out, ga, arm)
             cur = out
 
-    # one eager pass reserves all scratch (a graph must not allocate)
+    # eager warm-up passes reserve all scratch (a graph must not allocate)
     for i in range(warmup):
         step(i)
     hip.pipe_sync(0)
-
-    use_graph = not args.no_graph
     graph = None
     if use_graph:
         graph = hip.capture(0, lambda: [step(warmup + i) for i in range(steps)])
@@ -297,12 +327,13 @@ def main():
     wall = time.perf_counter() - t0
     gpu_ms = hip.event_elapsed(0, 0, 1)
     ms_per_step = wall * 1e3 / steps
+    del graph
 
     # distinct experts each step touches (for algorithmic bytes)
     ids = bids.download(np.int32, (n_all, S * k))[warmup:]
     distinct = float(np.mean([len(np.unique(r)) for r in ids]))
 
-    # profiled pass: per-kernel durations from HIP events on the device stream
+    # profiled pass: per-kernel execution times from the dispatch packets
     hip.reset_stats()
     hip.set_profile(True)
     for i in range(steps):
@@ -311,75 +342,119 @@ def main():
     hip.set_profile(False)
     ks = hip.kernel_stats()
 
-    # The profiled pass brackets every kernel with events on the device
-    # stream, so each duration also holds one event's own processing. That
-    # cost is measured here, in the same run: pairs of events with nothing
-    # between them, queued behind a long fill so they run back to back as the
-    # profiled kernels do (no waiting on the host in between).
-    backlog = hip.DeviceBuffer(256 << 20)
-    over = []
-    for _ in range(4):
-        backlog.fill(256 << 20, 0, 0.0, 0.0, 3)
-        for p in range(7):
-            hip.event_record(0, 2 + 2 * p)
-            hip.event_record(0, 3 + 2 * p)
-        over += [hip.event_elapsed(0, 2 + 2 * p, 3 + 2 * p) for p in range(7)]
-    ev_over_ms = float(np.median(over))
-    del backlog
-
-    gu_bytes, layer_bytes, gu_ops, layer_ops = algorithmic(cfg, args.wfmt, distinct)
+    gu_bytes, layer_bytes, gu_ops, layer_ops = algorithmic(cfg, wfmt, distinct)
     n_gu, ms_gu = ks["gateup"]
-    gu_raw_ms = ms_gu / max(n_gu, 1)
-    gu_ms = max(gu_raw_ms - ev_over_ms, 1e-6)
+    gu_ms = ms_gu / max(n_gu, 1)
     n_dn, ms_dn = ks["down"]
-    dn_ms = max(ms_dn / max(n_dn, 1) - ev_over_ms, 1e-6)
-    prefill = args.config == 4
+    dn_ms = ms_dn / max(n_dn, 1)
+    layer_ms = ms_per_step / L
+    prefill = cfg["S"] >= 1024
     if prefill:
         achieved = gu_ops / (gu_ms * 1e-3) / 1e12
         roof = dict(bound="mfma", achieved=round(achieved, 2), peak=INT8_PEAK_TOPS, unit="TFLOP/s",
-                    frac=round(achieved / INT8_PEAK_TOPS, 4), traffic=measured_traffic(cfg["name"]))
+                    frac=round(achieved / INT8_PEAK_TOPS, 4))
+        layer_frac = layer_ops / (layer_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS
     else:
         achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
         roof = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=round(achieved / HBM_PEAK_GBS, 4), traffic=measured_traffic(cfg["name"]))
-    value = S * L * steps / wall
+                    frac=round(achieved / HBM_PEAK_GBS, 4))
+        layer_frac = layer_bytes / (layer_ms * 1e-3) / 1e9 / HBM_PEAK_GBS
+    wl_name = cfg["name"] + ("_int8" if wfmt == "int8" else "")
+    roof["traffic"] = measured_traffic(wl_name)
+    roof["kernel"] = "gate/up (fused SwiGLU + h quant)"
+    roof["kernel_avg_us"] = round(gu_ms * 1e3, 2)
+    roof["layer_frac"] = round(layer_frac, 4)
+    summary = {
+        "workload": wl_name,
+        "value": round(S * L * steps / wall, 2),
+        "unit": "tokens/s",
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "gpu_event_ms_per_step": round(gpu_ms / steps, 4),
+        "roofline": roof,
+        "layer_GBps": round(layer_bytes / (layer_ms * 1e-3) / 1e9, 1),
+        "layer_TOPS": round(layer_ops / (layer_ms * 1e-3) / 1e12, 2),
+        "distinct_experts_per_step": distinct,
+        "kernel_avg_us": {name: round(ms / max(n, 1) * 1e3, 2) for name, (n, ms) in ks.items() if n},
+        "gateup_GBps": round(gu_bytes / (gu_ms * 1e-3) / 1e9, 1),
+        "down_GBps": round((layer_bytes - gu_bytes) / (dn_ms * 1e-3) / 1e9, 1) if n_dn else None,
+        "gateup_TOPS": round(gu_ops / (gu_ms * 1e-3) / 1e12, 2),
+        "down_TOPS": round((layer_ops - gu_ops) / (dn_ms * 1e-3) / 1e12, 2) if n_dn else None,
+        "setup_s": round(t_build, 1),
+    }
+    if pcie and S <= 64 and L == 1:
+        x0 = bx.download(np.float32, ((warmup + 1) * S, D))[warmup * S:]
+        summary["pcie_inclusive"] = pcie_inclusive(hip, cfg, layers[0][1], x0, ids[0],
+                                                   bw.download(np.float32, (n_all, S * k))[warmup], ga)
+    for b in (bx, bl, bids, bw, *bh):
+        b.free()
+    return summary, layers
+
+
+def main():
+    args = parse()
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1 "
+                                   "(no collectives or sharding in scope)"}))
+        sys.exit(2)
+    cfg = dict(CONFIGS[args.config])
+    if args.experts:
+        cfg["E"] = args.experts
+        cfg["name"] += f"_E{args.experts}"
+    cfg["seed"] = args.config
+    steps = args.steps if args.steps is not None else DEFAULT_STEPS[args.config]
+    warmup = args.warmup if args.warmup is not None else max(2, steps // 10)
+    from peregrine_amd import hip
+
+    assert hip.init([0]) == 1, "coli_hip_init failed"
+    arm = {"auto": -1, "gemv": hip.ARM_GEMV, "mfma": hip.ARM_MFMA}[args.arm]
+    ga = args.act_group
+    head, layers = run_workload(hip, cfg, args.wfmt, ga, arm, steps, warmup, use_graph=not args.no_graph,
+                                pcie=not args.no_pcie)
     line = {
         "metric": METRIC,
-        "value": round(value, 2),
+        "value": head["value"],
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8xint4" if args.wfmt == "int4" else "int8xint8",
         "data": "synthetic (seeded, device-generated weights; random-init experts)",
         "config": {
-            "workload": cfg["name"], "experts": E, "hidden": D, "moe_intermediate": cfg["I"], "tokens": S,
-            "top_k": k, "layers": L, "weights": f"{args.wfmt} QT, f32 scale per 32", "act_group": ga,
-            "arm": args.arm, "graph": use_graph, "parallelism": "none (1 GPU)",
+            "workload": head["workload"], "experts": cfg["E"], "hidden": cfg["D"], "moe_intermediate": cfg["I"],
+            "tokens": cfg["S"], "top_k": cfg["k"], "layers": cfg["layers"],
+            "weights": f"{args.wfmt} QT, f32 scale per 32", "act_group": ga, "arm": args.arm,
+            "graph": not args.no_graph, "parallelism": "none (1 GPU)",
         },
-        "roofline": roof,
-        "detail": {
-            "gpu_event_ms_per_step": round(gpu_ms / steps, 4),
-            "layer_GBps": round(layer_bytes * L / (ms_per_step * 1e-3) / 1e9, 1),
-            "layer_TOPS": round(layer_ops * L / (ms_per_step * 1e-3) / 1e12, 2),
-            "distinct_experts_per_step": distinct,
-            "kernel_avg_us": {name: round((ms / max(n, 1) - ev_over_ms) * 1e3, 2) for name, (n, ms) in ks.items() if n},
-            "event_bracket_overhead_us": round(ev_over_ms * 1e3, 2),
-            "gateup_event_us_raw": round(gu_raw_ms * 1e3, 2),
-            "gateup_GBps": round(gu_bytes / (gu_ms * 1e-3) / 1e9, 1),
-            "down_GBps": round((layer_bytes - gu_bytes) / (dn_ms * 1e-3) / 1e9, 1) if n_dn else None,
-            "gateup_TOPS": round(gu_ops / (gu_ms * 1e-3) / 1e12, 2),
-            "down_TOPS": round((layer_ops - gu_ops) / (dn_ms * 1e-3) / 1e12, 2) if n_dn else None,
-            "setup_s": round(t_build, 1),
-        },
+        "roofline": head["roofline"],
+        "detail": {k: v for k, v in head.items() if k not in ("value", "unit", "steps", "warmup", "ms_per_step",
+                                                             "roofline", "workload")},
     }
-    if S <= 64 and L == 1 and not args.no_pcie:
-        line["detail"]["pcie_inclusive"] = pcie_inclusive(hip, cfg, layers[0][1], bx, ids[0],
-                                                          bw.download(np.float32, (n_all, S * k))[warmup], warmup, ga)
+    if not args.no_detail:
+        # the decode (HBM) and prefill (MFMA) halves of the metric, on the
+        # 160-expert layer; config 4 reuses config 2's resident experts
+        del layers
+        wl = {}
+        shared = None
+        for cid in (2, 4):
+            if cid == args.config:
+                continue
+            c2 = dict(CONFIGS[cid])
+            c2["seed"] = 2
+            st = DEFAULT_STEPS[cid]
+            s, shared = run_workload(hip, c2, "int4", ga, -1, st, max(2, st // 10), layers=shared,
+                                     pcie=not args.no_pcie)
+            wl[s["workload"]] = s
+        line["detail"]["workloads"] = wl
+        del shared
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg, args.wfmt, ga, args.cpu_seconds)
     else:

@@ -89,7 +89,14 @@ int coli_hip_expert_group_reduce(ColiHipTensor *const *gates, ColiHipTensor *con
                                  const int *row_idx, const float *rw, int s_n, float *out,
                                  const float *x);                 /* coli_cuda_expert_group_reduce */
 
-/* ---- graphs: replaces backend_cuda.h:172-190 ---- */
+/* ---- graphs: replaces backend_cuda.h:172-190 ----
+ * With COLI_HIP_GRAPH=1 (or the reference's COLI_CUDA_GRAPH=1) in the
+ * environment, expert_group* calls are captured once per launch shape (arm,
+ * expert count, widths, rows per expert, reduce rows, formats) and replayed;
+ * descriptors and activations reach the graph through pinned staging that the
+ * replay copies, so a replay uses the current experts and inputs. Not cached:
+ * calls under profiling or with the debug-dot hook set (graph_cache_stats
+ * counts them as uncacheable). */
 int coli_hip_graph_begin(int device);                             /* coli_cuda_graph_begin */
 int coli_hip_graph_end(int device, ColiHipGraph **out);           /* coli_cuda_graph_end */
 /* graph_launch refuses (returns 0) a graph captured before the device's
@@ -188,12 +195,12 @@ void coli_hip_reset_stats(void);
  * also write every per-32-block int32 dot they compute: gate/up as
  * [R][2][I][ceil(D/32)], down as [R][D][ceil(I/32)]. */
 int coli_hip_set_debug_dots(int32_t *gateup_dev, int32_t *down_dev);
-/* Tuning hook: when set (device pointers, may be NULL), GEMV-arm workgroups
- * write 8 int64 per workgroup (index y*grid_x + x): phase timestamps of the
- * 100 MHz constant clock (entry, activations staged, first round ready, last
- * round ready, chain done, exit) and the hardware CU id. Library built with
- * -DPHIP_GEMV_TRACE only; otherwise ignored. */
-int coli_hip_set_debug_trace(long long *gateup_dev, long long *down_dev);
+/* Test hook: polls a GEMV's bounded wait (between its streaming waves and its
+ * chain wave) makes before giving up; 0 restores the default (2^22). A wait
+ * that gives up sets a host-visible flag: the next coli_hip_pipe_sync,
+ * coli_hip_graph_launch or expert_group* call on the device returns 0 with a
+ * diagnostic, and clears it. */
+int coli_hip_set_spin_limit(int polls);
 /* Last row plan of the device-resident path, copied to host (for tests):
  * hdr[4] = {rows, tiles, distinct experts, 0}. */
 int coli_hip_last_table(int device, int *hdr, int *uexp, int *off, int *row_tok, int *tok_rows, int e_cap,

@@ -15,12 +15,10 @@
 #include <stdlib.h>
 #include <string.h>
 
-/* exp rounded correctly to f32: computed in double (error < 1 double ulp) and
- * rounded once. glibc's expf, which Rust's f32::exp calls on Linux, returns the
- * same value except for inputs within ~0.002 ulp of a rounding midpoint. The GPU
- * kernels use the identical double-then-round construction, so the oracle and
- * the device agree bit-for-bit on silu/sigmoid/softmax. */
-static float exp_cr(float x) { return (float)exp((double)x); }
+/* exp as the reference evaluates it: Rust's f32::exp
+ * (crates/peregrine-model/src/math.rs:108-111) calls libm expf, which on Linux
+ * is glibc's. The oracle calls that same function. */
+static float ref_expf(float x) { return expf(x); }
 
 /* qrow_i8 — crates/peregrine-kernels/src/quant.rs:14-33. amax over |x|,
  * s = amax/127 floored at 1e-12, q = round_ties_even(x * (1/s)). Multiplying by
@@ -214,7 +212,7 @@ void orc_matmul_f32(float *y, const float *x, const float *w, int s_n, int d_n, 
 }
 
 /* siluf / silu_mul — crates/peregrine-model/src/math.rs:108-118. */
-float orc_silu(float x) { return x / (1.0f + exp_cr(-x)); }
+float orc_silu(float x) { return x / (1.0f + ref_expf(-x)); }
 
 void orc_silu_mul(float *g, const float *u, int n) {
     for (int i = 0; i < n; i++) g[i] = orc_silu(g[i]) * u[i];
@@ -290,13 +288,13 @@ int orc_negligible_tail(const float *w, int kept, float min_share) {
  * the lowest index, NaN never picked), weight = the sigmoid; unfilled slots
  * (0, 0); the negligible tail dropped (min_share > 0); optional renormalise
  * over all k slots with +1e-20; times routed_scale. sigmoid = 1/(1+exp(-x))
- * with exp evaluated as exp_cr. */
+ * with exp evaluated as ref_expf. */
 int orc_route_sigmoid(const float *logits, const float *bias, int s_n, int e_n, int k, int norm_topk,
                       float routed_scale, float min_share, int32_t *idx, float *w, int32_t *keff) {
     float *sig = malloc(sizeof(float) * e_n), *choice = malloc(sizeof(float) * e_n);
     for (int s = 0; s < s_n; s++) {
         for (int e = 0; e < e_n; e++) {
-            sig[e] = 1.0f / (1.0f + exp_cr(-logits[(size_t)s * e_n + e]));
+            sig[e] = 1.0f / (1.0f + ref_expf(-logits[(size_t)s * e_n + e]));
             choice[e] = sig[e] + bias[e];
         }
         int32_t *ib = idx + (size_t)s * k;
@@ -335,7 +333,7 @@ void orc_route_softmax_topk(const float *logits, int s_n, int e_n, int k, int32_
         int kept = greedy_topk(l, e_n, k, ib);
         float z = 0.0f;
         for (int kk = 0; kk < kept; kk++) {
-            ex[kk] = exp_cr(l[ib[kk]] - l[ib[0]]);
+            ex[kk] = ref_expf(l[ib[kk]] - l[ib[0]]);
             z += ex[kk];
         }
         for (int kk = 0; kk < kept; kk++) wb[kk] = ex[kk] / z;

@@ -75,7 +75,7 @@ SIGNATURES = {
     "coli_hip_kernel_stats": (None, [_i, _u64p, _dp]),
     "coli_hip_reset_stats": (None, []),
     "coli_hip_set_debug_dots": (_i, [_p, _p]),
-    "coli_hip_set_debug_trace": (_i, [_p, _p]),
+    "coli_hip_set_spin_limit": (_i, [_i]),
     "coli_hip_last_table": (_i, [_i, _ip, _ip, _ip, _ip, _ip, _i, _i]),
 }
 

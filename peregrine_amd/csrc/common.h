@@ -6,8 +6,11 @@
 // library is compiled with -ffp-contract=off so a*b+c never silently fuses.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "expf_glibc.h"
 
 namespace phip {
 
@@ -110,16 +113,6 @@ __device__ __forceinline__ __attribute__((address_space(1))) T *gptr_w(T *p) {
     return (__attribute__((address_space(1))) T *)p;
 }
 
-// Phase timestamp for the optional kernel trace (100 MHz constant clock),
-// taken after every outstanding memory operation of the wave has completed.
-#ifdef PHIP_GEMV_TRACE
-void set_misc_trace(long long *p);
-#endif
-__device__ __forceinline__ long long trace_stamp() {
-    __builtin_amdgcn_s_waitcnt(0);
-    return (long long)__builtin_amdgcn_s_memrealtime();
-}
-
 // Buffer-resource loads: a uniform descriptor (base, byte range) in SGPRs, a
 // 32-bit per-lane offset and a uniform 32-bit offset. No 64-bit address math
 // per load, and reads past the range return zero instead of faulting.
@@ -152,13 +145,10 @@ __device__ __forceinline__ bool grp_end(int b, int gshift, int nb) {
     return b + 1 == nb || (gshift < 30 && ((b + 1) & ((1 << gshift) - 1)) == 0);
 }
 
-// exp rounded once to f32 from a double-precision exp; equal to the correctly
-// rounded expf except within ~2^-28 of a midpoint. The oracle does the same.
-__device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x); }
-
-// siluf(x) * u — peregrine-model/src/math.rs:108-118 (division correctly rounded).
+// siluf(x) * u — peregrine-model/src/math.rs:108-118 (division correctly
+// rounded; exp with glibc expf's results, as Rust's f32::exp on Linux).
 __device__ __forceinline__ float silu_mul(float g, float u) {
-    float den = __fadd_rn(1.0f, exp_cr(-g));
+    float den = __fadd_rn(1.0f, expf_glibc(-g));
     return __fmul_rn(__fdiv_rn(g, den), u);
 }
 
@@ -213,6 +203,27 @@ __device__ __forceinline__ T warp_max(T v, int width) {
 
 // ---- host-side launchers (defined in the kernel translation units) ----
 namespace phip {
+// Kernel timing under profiling: the runtime arms a (start, stop) event pair
+// for a kernel slot; the slot's first launch records `start` and every launch
+// records `stop` inside its own dispatch packet (hipExtLaunchKernelGGL), so
+// the elapsed time is the kernels' execution alone, as a profiler's kernel
+// trace measures it, with no marker packets between them.
+struct LaunchTiming {
+    hipEvent_t start = nullptr, stop = nullptr;
+    bool used = false;
+};
+extern thread_local LaunchTiming g_launch_timing;
+template <typename K, typename... Args>
+inline void launch_k(K kern, dim3 grid, dim3 block, size_t lds, hipStream_t st, Args... args) {
+    LaunchTiming &t = g_launch_timing;
+    if (t.stop) {
+        hipExtLaunchKernelGGL(kern, grid, block, (uint32_t)lds, st, t.used ? nullptr : t.start, t.stop, 0u, args...);
+        t.used = true;
+    } else {
+        hipLaunchKernelGGL(kern, grid, block, lds, st, args...);
+    }
+}
+
 struct QuantArgs {
     const float *x; int x_stride; int rows; int K; int Kp;
     int8_t *q; int q_stride; float *s; int s_stride; int mode;
@@ -242,7 +253,8 @@ struct DotArgs {   // shared by the GEMV and MFMA arms
     int act_identity;                                                   // activation row = r (down proj)
     int act_zero;                                                       // activation row = 0 (one token)
     int n_rows_fixed;                                                   // >= 0: row count known on the host
-    long long *trace;                                                   // optional phase timestamps (tests/tuning)
+    int spin_limit;                                                     // GEMV: polls before a bounded wait gives up
+    int *wait_failed;                                                   // GEMV: host-visible word, set to 1 when one does
     int w_reuse;                                                        // MFMA arm: M tiles re-read each expert's weights
     RouteArgs route;                                                    // gate/up GEMV: logits != null -> fused router
 };
@@ -262,6 +274,9 @@ void launch_route_sigmoid(const float *logits, const float *bias, int S, int E, 
                           float routed_scale, float min_share, int *ids, float *w, int *keff, hipStream_t st);
 void launch_route_quant(const float *logits, int S, int E, int k, int *ids, float *w, const QuantArgs &a,
                         const ExpertDesc *desc, ExpertDesc *row_desc, hipStream_t st);
+// Polls a GEMV's bounded wait makes before it gives up (the default; a test
+// hook may lower it). 2^22 polls of >= 64 clocks each: ~0.1 s at 2.4 GHz.
+constexpr int GEMV_SPIN_LIMIT = 1 << 22;
 // LDS bytes one workgroup may use (device attribute), set at init.
 void set_lds_limit(int bytes);
 // one token: down GEMV + router-weighted combine in one launch (k rows in top-k order)

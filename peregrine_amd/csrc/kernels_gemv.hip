@@ -58,7 +58,7 @@ struct DStore<false> {
 };
 
 constexpr int GEMV_RING = 2;          // rounds of epilogue inputs held in LDS
-constexpr int GEMV_SPIN_LIMIT = 1 << 22;
+
 
 // dynamic LDS of the ring: [RING][NW*CH][64] f32 factors + the same count of dots
 template <bool W4, int NW, int CH>
@@ -66,11 +66,18 @@ __host__ __device__ constexpr size_t gemv_ring_bytes() {
     return ((size_t)GEMV_RING * NW * CH * 64 * (4 + (W4 ? 2 : 4)) + 15) / 16 * 16;
 }
 
-__device__ __forceinline__ void spin_until_geq(int *ctr, int target) {
-    for (int spin = 0; spin < GEMV_SPIN_LIMIT; ++spin) {
+// Waits until *ctr >= target for at most `limit` polls. On giving up (the
+// ring would be read or overwritten out of order, so the dispatch's output is
+// not valid) one lane stores 1 to the host-visible word `failed` and the wave
+// carries on, so every wave still reaches the end of the kernel; the host
+// reads the word after the stream synchronises and fails the call.
+__device__ __forceinline__ void spin_until_geq(int *ctr, int target, int limit, int *failed) {
+    for (int spin = 0;; ++spin) {
         if (__hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) return;
+        if (spin >= limit) break;
         __builtin_amdgcn_s_sleep(1);
     }
+    if ((threadIdx.x & 63) == 0) __hip_atomic_store(failed, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // NW streaming waves plus one chain wave. K is walked in rounds of NW*CH
@@ -106,14 +113,6 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemv_kernel(DotArgs a, MatGeom 
     const int wave = wave_id();
     const bool chainer = wave == NW;
     const int r = blockIdx.y;
-#ifdef PHIP_GEMV_TRACE
-    long long tr[6] = {0, 0, 0, 0, 0, 0};
-    const bool tracing = a.trace != nullptr && chainer;
-#else
-    long long tr[6];
-    constexpr bool tracing = false;
-#endif
-    if (tracing) tr[0] = trace_stamp();
     const int nrows = a.n_rows_fixed >= 0 ? a.n_rows_fixed : a.plan.counts[0];
     if (r >= nrows) return;  // uniform: fewer rows than the grid bound
 
@@ -128,24 +127,15 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemv_kernel(DotArgs a, MatGeom 
         constexpr int QSKIP = 4;
         const int tq = (int)threadIdx.x - 64 - (wave > QSKIP ? 64 : 0), nq = (NW - 1) * 64;
         float rmax = 0.0f;
-#ifdef PHIP_GEMV_TRACE
-        __shared__ long long r_tdone;
-#endif
         uint64_t mykey = 0, first = 0;   // wave 0: the selection, kept for the weights
         int kept = 0;
         if (wave == 0) {
-#ifdef PHIP_GEMV_TRACE
-            const long long tw = trace_stamp();
-#endif
             __builtin_amdgcn_s_setprio(3);   // the selection is every wave's critical path: issue it first
             // a workgroup needs picks 0..r only; the publishing one needs all k
             const int k_sel = blockIdx.x == 0 && r == 0 ? ra.k : r + 1;
             route_select<ROUTE_MAX_E / 64>(ra.logits, ra.E, k_sel, mykey, kept, first);
             __builtin_amdgcn_s_setprio(0);
             if (lane < k_sel) r_ids[lane] = lane < kept ? route_key_index(mykey) : 0;
-#ifdef PHIP_GEMV_TRACE
-            if (lane == 0) r_tdone = trace_stamp() - tw;
-#endif
         } else if (wave != QSKIP) {
             const uint4 *src = (const uint4 *)a.desc;
             uint4 *dst = (uint4 *)tdesc;
@@ -199,19 +189,9 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemv_kernel(DotArgs a, MatGeom 
                 }
             }
         }
-#ifdef PHIP_GEMV_TRACE
-        long long tq1 = tracing ? trace_stamp() : 0;
-#endif
         // the quantised row must be in L2 before any wave reads it as scalars
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-#ifdef PHIP_GEMV_TRACE
-        if (tracing && lane == 0) {
-            const long long tb = trace_stamp();
-            a.trace[((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 8 + 7] =
-                ((r_tdone) << 40) | ((tq1 - tr[0]) << 20) | (tb - tr[0]);
-        }
-#endif
         if (blockIdx.x == 0 && r == 0 && wave == 0)   // one workgroup publishes the routing
             route_weights(mykey, kept, first, ra.k, ra.ids, ra.w, tdesc, ra.row_desc);
         dsc = &tdesc[r_ids[r]];
@@ -267,21 +247,9 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemv_kernel(DotArgs a, MatGeom 
             if constexpr (EPI == EPI_B32) sxr[j] = sxs[b];
         }
     };
-#ifdef PHIP_GEMV_TRACE
-    long long tc0 = 0, tc1 = 0, tw0 = 0;
-#endif
     auto compute_round = [&](int c, const WBlk<W4> (&wv)[CH], const float (&sv)[CH]) {
-#ifdef PHIP_GEMV_TRACE
-        if (!ROUTE && a.trace && wave == 0 && c == 1) {
-            tw0 = trace_stamp();
-            // depend on the first and last weight words: the round's loads have landed
-            const int probe = __builtin_amdgcn_readfirstlane((int)(wv[0].a.x ^ wv[CH - 1].a.w));
-            asm volatile("; trace probe %0" ::"s"(probe));
-            tc0 = trace_stamp();
-        }
-#endif
         // the ring slot of round c is free once the chain finished round c - RING
-        if (c >= GEMV_RING) spin_until_geq(&consumed, c - GEMV_RING + 1);
+        if (c >= GEMV_RING) spin_until_geq(&consumed, c - GEMV_RING + 1, a.spin_limit, a.wait_failed);
         const int slot = (c % GEMV_RING) * SLOT;
         // No per-block guard: blocks past nb (the last round's tail) read the
         // last block's activations and fill ring slots the chain never reads.
@@ -309,22 +277,12 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemv_kernel(DotArgs a, MatGeom 
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         if (lane == 0)
             __hip_atomic_fetch_add(&produced[c % GEMV_RING], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-#ifdef PHIP_GEMV_TRACE
-        if (!ROUTE && a.trace && wave == 0 && c == 1) {
-            tc1 = trace_stamp();
-            if (lane == 0) {
-                long long *dst = a.trace + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 8;
-                dst[7] = ((tc0 - tw0) << 32) | (tc1 - tc0);   // wait for loads, compute (100 MHz ticks)
-            }
-        }
-#endif
     };
 
     if (threadIdx.x < GEMV_RING) produced[threadIdx.x] = 0;
     if (threadIdx.x == 0) consumed = 0;
     if (!chainer) load_round(0, wA, sA);
     __syncthreads();
-    if (tracing) tr[1] = trace_stamp();
 
     float facc = 0.0f;   // chain accumulator (chain wave)
     int gsum = 0;        // EPI_GRP: open group's integer sum
@@ -338,11 +296,7 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemv_kernel(DotArgs a, MatGeom 
     } else {
 #pragma unroll 1
         for (int c = 0; c < nrounds; ++c) {
-            spin_until_geq(&produced[c % GEMV_RING], NW * (c / GEMV_RING + 1));
-            if (tracing) {
-                if (c == 0) tr[2] = trace_stamp();
-                tr[3] = trace_stamp();
-            }
+            spin_until_geq(&produced[c % GEMV_RING], NW * (c / GEMV_RING + 1), a.spin_limit, a.wait_failed);
             const int slot = (c % GEMV_RING) * SLOT;
             const int lo = c * RB, n = min(nb, lo + RB) - lo;
             const float *fr = lds_f + slot + lane;   // block q of the round at [q * 64]
@@ -386,7 +340,6 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemv_kernel(DotArgs a, MatGeom 
             if (lane == 0) __hip_atomic_store(&consumed, c + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     }
-    if (tracing) tr[4] = trace_stamp();
 
     if (!chainer) return;
     float v;
@@ -414,14 +367,6 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemv_kernel(DotArgs a, MatGeom 
         }
     } else {
         if (o < g.O) a.out[(size_t)r * a.out_stride + o] = v;
-    }
-    if (tracing) {
-        tr[5] = trace_stamp();
-        if (lane == 0) {
-            long long *dst = a.trace + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 8;
-            for (int i = 0; i < 6; ++i) dst[i] = tr[i];
-            dst[6] = (long long)__smid();
-        }
     }
 }
 
@@ -563,7 +508,7 @@ bool gemv_down_combine_ok(const MatGeom &g, int k) {
 template <bool W4, int EPI>
 static void launch_dc(const DotArgs &a, const MatGeom &g, int k, const float *w, float *out, hipStream_t st) {
     const dim3 grid((unsigned)((g.O + 15) / 16)), block((unsigned)(64 * k));
-    hipLaunchKernelGGL((gemv_down_combine_kernel<W4, EPI>), grid, block, 0, st, a, g, k, w, out);
+    launch_k((gemv_down_combine_kernel<W4, EPI>), grid, block, 0, st, a, g, k, w, out);
 }
 
 void launch_gemv_down_combine(const DotArgs &a, const MatGeom &g, int act, int k, const float *w, float *out,
@@ -597,7 +542,7 @@ static void launch_gemv_c(const DotArgs &a, const MatGeom &g, int grid_rows, hip
     static size_t opted[LDS_OPT_DEVICES];
     lds_opt_in((const void *)kern, lds, opted);
     dim3 grid(GATEUP ? (unsigned)((g.O + 31) / 32) : (unsigned)((g.O + 63) / 64), (unsigned)grid_rows);
-    hipLaunchKernelGGL(kern, grid, dim3((NW + 1) * 64), lds, st, a, g, a.xq, a.sx);
+    launch_k(kern, grid, dim3((NW + 1) * 64), lds, st, a, g, a.xq, a.sx);
 }
 
 template <bool W4, int EPI, bool GATEUP>

@@ -569,7 +569,7 @@ static void launch_mfma_p(const DotArgs &a, const MatGeom &g, int grid_tiles, hi
     const int span = GATEUP ? ((g.O + 31) & ~31) : g.O;
     dim3 grid((unsigned)((span + ch_per_wg - 1) / ch_per_wg), (unsigned)grid_tiles);
     const size_t lds = EPI == EPI_B32 ? (size_t)g.nb * 32 * sizeof(float) : 0;
-    hipLaunchKernelGGL((mfma_kernel<W4, EPI, GATEUP, NSUB, PD>), grid, dim3(256), lds, st, a, g, a.xq, a.sx);
+    launch_k((mfma_kernel<W4, EPI, GATEUP, NSUB, PD>), grid, dim3(256), lds, st, a, g, a.xq, a.sx);
 }
 
 // stages plus (per-32 activation scales) the tile's scales
@@ -596,7 +596,7 @@ static void launch_mfma_dma_h(const DotArgs &a, const MatGeom &g, int grid_tiles
     auto kern = mfma_dma_kernel<W4, EPI, GATEUP, NSUB, PD, WNT>;
     static size_t opted[LDS_OPT_DEVICES];
     lds_opt_in((const void *)kern, lds, opted);
-    hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, a, g);
+    launch_k(kern, grid, dim3(256), lds, st, a, g);
 }
 
 // Weights are copied non-temporally unless the dispatch re-reads them (about

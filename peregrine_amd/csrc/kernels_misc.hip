@@ -63,10 +63,10 @@ __global__ __launch_bounds__(256) void quant_blocks_kernel(QuantArgs a) {
 void launch_quant_rows(const QuantArgs &a, hipStream_t st) {
     if (a.rows <= 0) return;
     if (a.mode == ACT_ROW) {
-        hipLaunchKernelGGL(quant_rows_kernel, dim3(a.rows), dim3(1024), 0, st, a);
+        launch_k(quant_rows_kernel, dim3(a.rows), dim3(1024), 0, st, a);
     } else {
         const int nb = a.Kp / BLK;
-        hipLaunchKernelGGL(quant_blocks_kernel, dim3((unsigned)((nb + 63) / 64), (unsigned)a.rows), dim3(256), 0, st,
+        launch_k(quant_blocks_kernel, dim3((unsigned)((nb + 63) / 64), (unsigned)a.rows), dim3(256), 0, st,
                            a);
     }
 }
@@ -127,7 +127,7 @@ __global__ void repack_kernel(const uint8_t *raw, const float *raw_sc, int fmt, 
 void launch_repack(const uint8_t *raw, const float *raw_sc, int fmt, int I, int O, int gs, uint8_t *w, float *sc,
                    const MatGeom &g, hipStream_t st) {
     const size_t total = (size_t)g.Op * g.nb;
-    hipLaunchKernelGGL(repack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, raw, raw_sc, fmt, I,
+    launch_k(repack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, raw, raw_sc, fmt, I,
                        O, gs, w, sc, g);
 }
 
@@ -150,16 +150,6 @@ __global__ __launch_bounds__(256) void combine_csr_kernel(float *out, const floa
     out[(size_t)s * D + d] = acc;
 }
 
-#ifdef PHIP_GEMV_TRACE
-// debug timeline of the router/quant and combine kernels: [start, mid, end] per workgroup
-__device__ long long *g_misc_trace;
-void set_misc_trace(long long *p) { (void)hipMemcpyToSymbol(HIP_SYMBOL(g_misc_trace), &p, sizeof(p)); }
-#define MISC_STAMP(slot, i) \
-    do { if (g_misc_trace && threadIdx.x == 0) g_misc_trace[(slot) * 4 + (i)] = trace_stamp(); } while (0)
-#else
-#define MISC_STAMP(slot, i) do {} while (0)
-#endif
-
 // Device-table form: token s adds its rows tok_rows[s*k + j] (union order,
 // -1 terminates) weighted by w[s*k + tok_kk[s*k + j]] — the reference scatter
 // out[s] += w * y (mlp.rs:111-119) from a zero row.
@@ -171,7 +161,6 @@ __global__ __launch_bounds__(256) void combine_tok_kernel(float *out, const floa
                                                           const int *tok_kk, const float *w, int k, int D,
                                                           int y_stride, int vec4) {
     const int s = blockIdx.y;
-    MISC_STAMP(1000 + blockIdx.x, 0);
     const int d0 = (blockIdx.x * 256 + threadIdx.x) * 4;
     // The token's row list and weights: every index load is issued before
     // any is used (clamped, unconditional), then every weight load.
@@ -209,7 +198,6 @@ __global__ __launch_bounds__(256) void combine_tok_kernel(float *out, const floa
             }
         }
         *(float4 *)(out + (size_t)s * D + d0) = acc;
-        MISC_STAMP(1000 + blockIdx.x, 2);
     } else {
         for (int d = d0; d < min(D, d0 + 4); d++) {
             float acc = 0.0f;
@@ -222,7 +210,7 @@ __global__ __launch_bounds__(256) void combine_tok_kernel(float *out, const floa
 void launch_combine(float *out, const float *y, const int *row_ptr, const int *row_idx, const float *rw, int s_n,
                     int D, int y_stride, hipStream_t st) {
     if (s_n <= 0) return;
-    hipLaunchKernelGGL(combine_csr_kernel, dim3((unsigned)((D + 255) / 256), (unsigned)s_n), dim3(256), 0, st, out,
+    launch_k(combine_csr_kernel, dim3((unsigned)((D + 255) / 256), (unsigned)s_n), dim3(256), 0, st, out,
                        y, row_ptr, row_idx, rw, D, y_stride);
 }
 
@@ -230,7 +218,7 @@ void launch_combine_tok(float *out, const float *y, const int *tok_rows, const i
                         int k, int D, int y_stride, hipStream_t st) {
     if (s_n <= 0) return;
     const int vec4 = (D % 4 == 0 && y_stride % 4 == 0) ? 1 : 0;
-    hipLaunchKernelGGL(combine_tok_kernel, dim3((unsigned)((D + 1023) / 1024), (unsigned)s_n), dim3(256), 0, st, out,
+    launch_k(combine_tok_kernel, dim3((unsigned)((D + 1023) / 1024), (unsigned)s_n), dim3(256), 0, st, out,
                        y, tok_rows, tok_kk, w, k, D, y_stride, vec4);
 }
 
@@ -253,7 +241,7 @@ __global__ __launch_bounds__(64) void route_sigmoid_kernel(const float *logits, 
         const int e = lane + 64 * j;
         float c = -INFINITY, sig = 0.0f;
         if (e < E) {
-            sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, exp_cr(-l[e])));
+            sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc(-l[e])));
             c = __fadd_rn(sig, bias ? bias[e] : 0.0f);
         }
         sg[j] = sig;
@@ -326,7 +314,7 @@ void launch_route_sigmoid(const float *logits, const float *bias, int S, int E, 
     if (S <= 0) return;
     const dim3 g((unsigned)S), b(64);
 #define PHIP_ROUTE_SIG(P) \
-    hipLaunchKernelGGL(route_sigmoid_kernel<P>, g, b, 0, st, logits, bias, E, k, norm_topk, routed_scale, min_share, \
+    launch_k(route_sigmoid_kernel<P>, g, b, 0, st, logits, bias, E, k, norm_topk, routed_scale, min_share, \
                        ids, w, keff)
     if (E <= 64) PHIP_ROUTE_SIG(1);
     else if (E <= 128) PHIP_ROUTE_SIG(2);
@@ -353,11 +341,9 @@ __global__ __launch_bounds__(256) void route_quant_kernel(const float *logits, i
                                                           ExpertDesc *row_desc) {
     __shared__ float red[4];
     const int s = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-    MISC_STAMP(blockIdx.y, 0);
     if (blockIdx.y == 0 && wave == 0) {
         route_token<PER>(logits + (size_t)s * E, E, k, ids + (size_t)s * k, w + (size_t)s * k, desc,
                          row_desc ? row_desc + (size_t)s * k : nullptr);
-        MISC_STAMP(blockIdx.y, 1);
     }
     const float *x = a.x + (size_t)s * a.x_stride;
     int8_t *q = a.q + (size_t)s * a.q_stride;
@@ -372,7 +358,6 @@ __global__ __launch_bounds__(256) void route_quant_kernel(const float *logits, i
         } else {
             quant_row_b32(x, a.K, a.Kp, q, a.s + (size_t)s * a.s_stride, 4 * b_lo, 4 * b_hi, tid, 256);
         }
-        MISC_STAMP(blockIdx.y, 2);
     } else {
         constexpr int PX = 32;   // K <= 8192 from registers, the rest re-read
         float v[PX];
@@ -411,7 +396,7 @@ static void route_quant_t(const float *logits, int S, int E, int k, int *ids, fl
     // token); many tokens: one workgroup per token
     const int nbk = a.Kp / BLK;
     const int slabs = a.mode == ACT_B32 ? std::max(1, std::min((nbk + 7) / 8, 256 / S)) : 1;
-    hipLaunchKernelGGL(route_quant_kernel<PER>, dim3((unsigned)S, (unsigned)slabs), dim3(256), 0, st, logits, E, k,
+    launch_k(route_quant_kernel<PER>, dim3((unsigned)S, (unsigned)slabs), dim3(256), 0, st, logits, E, k,
                        ids, w, a, desc, row_desc);
 }
 
@@ -428,11 +413,11 @@ void launch_route_quant(const float *logits, int S, int E, int k, int *ids, floa
 void launch_route_softmax(const float *logits, int S, int E, int k, int *ids, float *w, hipStream_t st) {
     if (S <= 0) return;
     const dim3 g((unsigned)S), b(64);
-    if (E <= 64) hipLaunchKernelGGL(route_softmax_kernel<1>, g, b, 0, st, logits, E, k, ids, w);
-    else if (E <= 128) hipLaunchKernelGGL(route_softmax_kernel<2>, g, b, 0, st, logits, E, k, ids, w);
-    else if (E <= 256) hipLaunchKernelGGL(route_softmax_kernel<4>, g, b, 0, st, logits, E, k, ids, w);
-    else if (E <= 512) hipLaunchKernelGGL(route_softmax_kernel<8>, g, b, 0, st, logits, E, k, ids, w);
-    else hipLaunchKernelGGL(route_softmax_kernel<16>, g, b, 0, st, logits, E, k, ids, w);
+    if (E <= 64) launch_k(route_softmax_kernel<1>, g, b, 0, st, logits, E, k, ids, w);
+    else if (E <= 128) launch_k(route_softmax_kernel<2>, g, b, 0, st, logits, E, k, ids, w);
+    else if (E <= 256) launch_k(route_softmax_kernel<4>, g, b, 0, st, logits, E, k, ids, w);
+    else if (E <= 512) launch_k(route_softmax_kernel<8>, g, b, 0, st, logits, E, k, ids, w);
+    else launch_k(route_softmax_kernel<16>, g, b, 0, st, logits, E, k, ids, w);
 }
 
 // ---------------------------------------------------------------------------
@@ -787,15 +772,15 @@ void launch_build_table(const int *ids, int S, int k, int E, const TableOut &t, 
                         hipStream_t st) {
     const int tpc = TBL_CHUNK / k, G = table_chunks(S, k), N = S * k;
     if (N <= TBL_SMALL) {
-        hipLaunchKernelGGL(table_small_kernel, dim3(1), dim3(TBL_SMALL), 0, st, ids, N, k, E, t, tmax);
+        launch_k(table_small_kernel, dim3(1), dim3(TBL_SMALL), 0, st, ids, N, k, E, t, tmax);
         return;
     }
     int *firstg = work, *cntg = firstg + (size_t)G * E, *erank = cntg + (size_t)G * E, *ebase = erank + E;
     if (G > 0)
-        hipLaunchKernelGGL(table_count_kernel, dim3(G), dim3(TBL_CHUNK), 0, st, ids, N, k, E, tpc, firstg, cntg);
-    hipLaunchKernelGGL(table_scan_kernel, dim3(1), dim3(1024), 0, st, E, G, firstg, cntg, erank, ebase, t, tmax);
+        launch_k(table_count_kernel, dim3(G), dim3(TBL_CHUNK), 0, st, ids, N, k, E, tpc, firstg, cntg);
+    launch_k(table_scan_kernel, dim3(1), dim3(1024), 0, st, E, G, firstg, cntg, erank, ebase, t, tmax);
     if (G > 0)
-        hipLaunchKernelGGL(table_place_kernel, dim3(G), dim3(TBL_CHUNK), 0, st, ids, N, k, E, tpc, cntg, erank, ebase,
+        launch_k(table_place_kernel, dim3(G), dim3(TBL_CHUNK), 0, st, ids, N, k, E, tpc, cntg, erank, ebase,
                            t);
 }
 
@@ -841,7 +826,7 @@ void launch_synth_fill(void *dst, size_t n, int kind, float a, float b, uint64_t
     const size_t items = kind == 0 ? (n + 7) / 8 : n;
     size_t blocks = (items + 255) / 256;
     if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(synth_fill_kernel, dim3((unsigned)blocks), dim3(256), 0, st, dst, n, kind, a, b, seed);
+    launch_k(synth_fill_kernel, dim3((unsigned)blocks), dim3(256), 0, st, dst, n, kind, a, b, seed);
 }
 
 }  // namespace phip

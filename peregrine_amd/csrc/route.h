@@ -146,7 +146,7 @@ __device__ __forceinline__ void route_weights(uint64_t mykey, int kept, uint64_t
                                               const ExpertDesc *desc, ExpertDesc *row_desc) {
     const int lane = threadIdx.x & 63;
     const float l0 = route_key_value(first);
-    const float myex = lane < kept ? exp_cr(__fsub_rn(route_key_value(mykey), l0)) : 0.0f;
+    const float myex = lane < kept ? expf_glibc(__fsub_rn(route_key_value(mykey), l0)) : 0.0f;
     float z = 0.0f;
     for (int kk = 0; kk < kept; kk++)
         z = __fadd_rn(z, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(myex), kk)));

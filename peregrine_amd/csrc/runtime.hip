@@ -52,8 +52,17 @@ struct Buf {
     size_t cap = 0;
 };
 
-constexpr int GRAPH_CACHE = 16;
-constexpr int N_EVENTS = 2 * COLI_HIP_K_COUNT + 4;
+constexpr int GRAPH_CACHE = 16;   // cached expert-group graphs per device
+constexpr int N_EVENTS = 2 * (COLI_HIP_K_COUNT + 4);   // (start, stop) per kernel slot of a dispatch
+
+// One cached expert-group graph: its launch-shape key, the scratch generation
+// it was captured under and its last use (least recently used is evicted).
+struct GraphSlot {
+    uint64_t key = 0;
+    ColiHipGraph *g = nullptr;
+    unsigned gen = 0;
+    uint64_t used = 0;
+};
 
 struct Ctx {
     int device = -1;
@@ -63,7 +72,13 @@ struct Ctx {
     Buf xq, sx, h, hq, sh, y, red_out, meta, tbl, rdesc;
     Buf pin_x, pin_y, pin_meta;
     hipEvent_t ev[N_EVENTS] = {};
+    hipEvent_t phase_ev[4] = {};   // expert_group phases under profiling: H2D | kernels | D2H
     hipEvent_t user_ev[16] = {};
+    // Host-visible word a GEMV sets when one of its bounded waits gives up
+    // (mapped pinned memory: the host reads it after a stream synchronise).
+    int *wait_flag = nullptr, *wait_flag_dev = nullptr;
+    GraphSlot graphs[GRAPH_CACHE];
+    uint64_t graph_clock = 0;
     // last device-resident table (for coli_hip_last_table)
     TableOut tbl_view{};
     int tbl_E = 0, tbl_R = 0;
@@ -73,16 +88,19 @@ Ctx g_ctx[COLI_HIP_MAX_DEVICES];
 int g_nctx = 0;
 std::mutex g_stats_mu;
 uint64_t g_calls = 0, g_experts = 0, g_rows = 0;
-double g_h2d_ms = 0, g_kernel_ms = 0, g_d2h_ms = 0;
+double g_h2d_ms = 0, g_d2h_ms = 0;   // expert_group phases, under profiling
 uint64_t g_k_launches[COLI_HIP_K_COUNT] = {};
 double g_k_ms[COLI_HIP_K_COUNT] = {};
 uint64_t g_graph_captures = 0, g_graph_replays = 0, g_graph_invalidations = 0, g_graph_uncacheable = 0;
 int g_act_group = -1;   // -1: read COLI_HIP_ACT_GROUP on first use
 int g_arm = -2;         // -2: read COLI_HIP_ARM on first use
 int g_profile = -1;
+int g_spin_limit = GEMV_SPIN_LIMIT;
 int32_t *g_dbg_gu = nullptr, *g_dbg_dn = nullptr;
-long long *g_trace_gu = nullptr, *g_trace_dn = nullptr;
 thread_local int g_cur_dev = -1;
+}  // namespace
+thread_local phip::LaunchTiming phip::g_launch_timing;
+namespace {
 
 int hip_ok(hipError_t e, const char *what) {
     if (e == hipSuccess) return 1;
@@ -243,6 +261,15 @@ int select_ctx(Ctx *c) {
     return 1;
 }
 
+// After the device's stream has synchronised: fails (0) if a GEMV bounded
+// wait gave up since the last check, and clears the flag.
+int check_waits(Ctx *c) {
+    if (!c->wait_flag || !*(volatile int *)c->wait_flag) return 1;
+    *(volatile int *)c->wait_flag = 0;
+    return fail("GEMV: a bounded wait between the streaming and chain waves gave up; the output of the "
+                "dispatches since the last check is not valid");
+}
+
 // Grow-only device scratch. A reallocation bumps the generation so anything
 // holding baked addresses (captured graphs) knows it is stale.
 // Scratch must not move while a capture is recording addresses into it.
@@ -277,7 +304,23 @@ int reserve_pinned(Ctx *c, Buf &b, size_t bytes) {
     return 1;
 }
 
+void graph_destroy(ColiHipGraph *g) {
+    if (!g) return;
+    if (g->exec) hipGraphExecDestroy(g->exec);
+    if (g->graph) hipGraphDestroy(g->graph);
+    std::free(g);
+}
+
+// Drops every cached expert-group graph of a device.
+void graph_cache_clear(Ctx *c) {
+    for (GraphSlot &sl : c->graphs) {
+        graph_destroy(sl.g);
+        sl = GraphSlot{};
+    }
+}
+
 void free_ctx(Ctx *c) {
+    graph_cache_clear(c);
     Buf *dev[] = {&c->xq, &c->sx, &c->h, &c->hq, &c->sh, &c->y, &c->red_out, &c->meta, &c->tbl, &c->rdesc};
     for (Buf *b : dev) {
         if (b->p) hipFree(b->p);
@@ -298,6 +341,13 @@ void free_ctx(Ctx *c) {
             hipEventDestroy(e);
             e = nullptr;
         }
+    for (auto &e : c->phase_ev)
+        if (e) {
+            hipEventDestroy(e);
+            e = nullptr;
+        }
+    if (c->wait_flag) hipHostFree(c->wait_flag);
+    c->wait_flag = c->wait_flag_dev = nullptr;
     if (c->stream) hipStreamDestroy(c->stream);
     c->stream = nullptr;
 }
@@ -430,30 +480,42 @@ void note_group(int count, int total) {
     g_rows += (uint64_t)total;
 }
 
-// Records kernel-boundary events when profiling; accumulates at finish().
+// Kernel durations under profiling: mark(w) arms an event pair that the
+// launches of slot w record inside their dispatch packets (launch_k); mark(-1)
+// disarms. finish() waits and accumulates the slots that launched anything.
 struct Prof {
     Ctx *c;
     bool on;
     int n = 0;
-    int which[N_EVENTS];
+    int which[N_EVENTS / 2];
+    bool used[N_EVENTS / 2];
     explicit Prof(Ctx *ctx) : c(ctx), on(profiling() != 0) {
         if (!on) return;
         for (auto &e : c->ev)
             if (!e && hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) on = false;
     }
-    void mark(int w) {   // event before kernel w (w = -1: final)
-        if (!on || n >= N_EVENTS) return;
+    ~Prof() { g_launch_timing = LaunchTiming{}; }
+    void close_slot() {
+        if (n > 0) used[n - 1] = g_launch_timing.used;
+        g_launch_timing = LaunchTiming{};
+    }
+    void mark(int w) {   // the launches that follow belong to kernel slot w (w = -1: none)
+        if (!on) return;
+        close_slot();
+        if (w < 0 || n >= N_EVENTS / 2) return;
         which[n] = w;
-        hipEventRecord(c->ev[n++], c->stream);
+        used[n] = false;
+        g_launch_timing = LaunchTiming{c->ev[2 * n], c->ev[2 * n + 1], false};
+        n++;
     }
     void finish() {
-        if (!on || n < 2) return;
-        hipEventSynchronize(c->ev[n - 1]);
+        if (!on) return;
+        close_slot();
+        if (n == 0 || hipStreamSynchronize(c->stream) != hipSuccess) return;
         std::lock_guard<std::mutex> lock(g_stats_mu);
-        for (int i = 0; i + 1 < n; i++) {
+        for (int i = 0; i < n; i++) {
             float ms = 0;
-            if (which[i] < 0) continue;
-            hipEventElapsedTime(&ms, c->ev[i], c->ev[i + 1]);
+            if (!used[i] || hipEventElapsedTime(&ms, c->ev[2 * i], c->ev[2 * i + 1]) != hipSuccess) continue;
             g_k_launches[which[i]]++;
             g_k_ms[which[i]] += ms;
         }
@@ -526,12 +588,13 @@ void run_experts(Ctx *c, Prof &prof, const ExpertDesc *desc, const RowPlan &plan
     da.sh = s.sh;
     da.sh_stride = s.shs;
     da.dots = g_dbg_gu;
-    da.trace = g_trace_gu;
     da.act_identity = x_identity ? 1 : 0;
     da.act_zero = opt.act_zero ? 1 : 0;
     da.n_rows_fixed = opt.n_rows_fixed;
     da.route = opt.route;
     da.w_reuse = opt.w_reuse;
+    da.spin_limit = g_spin_limit;
+    da.wait_failed = c->wait_flag_dev;
     prof.mark(COLI_HIP_K_GATEUP);
     if (arm == COLI_HIP_ARM_GEMV)
         launch_gemv_gateup(da, gg, act, R_bound, c->stream);
@@ -554,7 +617,6 @@ void run_experts(Ctx *c, Prof &prof, const ExpertDesc *desc, const RowPlan &plan
     dd.hq = nullptr;
     dd.sh = nullptr;
     dd.dots = g_dbg_dn;
-    dd.trace = g_trace_dn;
     dd.act_identity = 1;
     dd.act_zero = 0;
     dd.route = RouteArgs{};
@@ -574,6 +636,82 @@ struct ReduceSpec {
     int s_n;
     float *out;
 };
+
+// ---------------------------------------------------------------------------
+// Expert-group graph cache (COLI_HIP_GRAPH=1, or COLI_CUDA_GRAPH=1 as the
+// reference's knob). A decode loop calls expert_group with the same launch
+// shape (arm, expert count, widths, rows per expert) over and over while the
+// contents change: which experts (their descriptors) and the activations.
+// The shape becomes one captured graph; the contents ride in through the
+// pinned staging buffers that the graph's own H2D copies read, so one graph
+// serves every later call of that shape (backend_cuda.cu:666-745, 1104-1166).
+// A slot keeps the full shape, not only its hash, so two shapes never share
+// a graph. A graph captured before a scratch reallocation is dropped at
+// lookup (its baked addresses are stale); a failed capture drops them all.
+// ---------------------------------------------------------------------------
+bool graph_cache_enabled() {
+    const char *v = std::getenv("COLI_HIP_GRAPH");
+    if (!v || !*v) v = std::getenv("COLI_CUDA_GRAPH");
+    return v && std::atoi(v) != 0;
+}
+
+struct ShapeKey {
+    std::vector<int> v;
+    uint64_t hash = 0;
+};
+
+ShapeKey shape_key(const std::vector<int> &fields, const int *rows, int count) {
+    ShapeKey k;
+    k.v = fields;
+    k.v.insert(k.v.end(), rows, rows + count);
+    uint64_t h = 0xcbf29ce484222325ull;   // FNV-1a, 64-bit
+    for (int x : k.v)
+        for (int b = 0; b < 4; b++) {
+            h ^= (uint64_t)((uint32_t)x >> (8 * b)) & 0xff;
+            h *= 0x100000001b3ull;
+        }
+    k.hash = h;
+    return k;
+}
+
+std::vector<int> g_slot_shape[COLI_HIP_MAX_DEVICES][GRAPH_CACHE];
+
+ColiHipGraph *graph_lookup(Ctx *c, const ShapeKey &key) {
+    const int ci = (int)(c - g_ctx);
+    for (int i = 0; i < GRAPH_CACHE; i++) {
+        GraphSlot &sl = c->graphs[i];
+        if (!sl.g || sl.key != key.hash || g_slot_shape[ci][i] != key.v) continue;
+        if (sl.gen != c->gen) {   // scratch moved since the capture
+            graph_destroy(sl.g);
+            sl = GraphSlot{};
+            std::lock_guard<std::mutex> lock(g_stats_mu);
+            g_graph_invalidations++;
+            return nullptr;
+        }
+        sl.used = ++c->graph_clock;
+        return sl.g;
+    }
+    return nullptr;
+}
+
+void graph_store(Ctx *c, const ShapeKey &key, ColiHipGraph *g) {
+    const int ci = (int)(c - g_ctx);
+    int victim = 0;
+    for (int i = 0; i < GRAPH_CACHE; i++) {
+        if (!c->graphs[i].g) {
+            victim = i;
+            break;
+        }
+        if (c->graphs[i].used < c->graphs[victim].used) victim = i;
+    }
+    GraphSlot &sl = c->graphs[victim];
+    graph_destroy(sl.g);
+    sl.key = key.hash;
+    sl.g = g;
+    sl.gen = c->gen;
+    sl.used = ++c->graph_clock;
+    g_slot_shape[ci][victim] = key.v;
+}
 
 int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, ColiHipTensor *const *downs,
                       const int *rows, int count, float *y, const float *x, const ReduceSpec *red, int *arm_out) {
@@ -613,12 +751,15 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
     const size_t meta_b = desc_b + n_int * 4 + (red ? (size_t)total * 4 : 0);
     const size_t xb = (size_t)total * D * 4;
     const size_t ob = red ? (size_t)s_n * D * 4 : xb;
+    // every reservation happens here, before any capture (scratch must not
+    // move while a graph records its addresses)
     Scratch s{};
     if (!reserve_rows(c, gg, gd, total, total, ga, &s) || !reserve(c, c->meta, meta_b) ||
         !reserve_pinned(c, c->pin_meta, meta_b) || !reserve_pinned(c, c->pin_x, xb) ||
         !reserve_pinned(c, c->pin_y, ob) || (red && !reserve(c, c->red_out, ob)))
         return 0;
 
+    // stage the call's contents: descriptors, row plan, reduce layout, x
     uint8_t *hm = (uint8_t *)c->pin_meta.p;
     ExpertDesc *hd = (ExpertDesc *)hm;
     for (int i = 0; i < count; i++) {
@@ -652,16 +793,7 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
     }
     std::memcpy(c->pin_x.p, x, xb);
 
-    Prof prof(c);
-    prof.mark(-1);
     uint8_t *dm = (uint8_t *)c->meta.p;
-    if (!hip_ok(hipMemcpyAsync(dm, hm, meta_b, hipMemcpyHostToDevice, c->stream), "expert group metadata"))
-        return 0;
-    // x ([total][D] f32) is staged in the y buffer, which has exactly that
-    // shape: the x quantisation reads it before the down projection writes y.
-    float *x_dev = (float *)c->y.p;
-    if (!hip_ok(hipMemcpyAsync(x_dev, c->pin_x.p, xb, hipMemcpyHostToDevice, c->stream), "expert group input upload"))
-        return 0;
     int *di = (int *)(dm + desc_b);
     RowPlan plan{};
     plan.row_exp = di;
@@ -672,24 +804,106 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
     plan.counts = di + total + 3 * T;
     DispatchOpts opt;
     opt.w_reuse = total >= 2 * MT_ROWS * count;   // about two or more M tiles per expert
-    run_experts(c, prof, (const ExpertDesc *)dm, plan, gg, gd, x_dev, total, true, total, T, ga, arm, s, opt);
-    float *res = s.y;
-    if (red) {
-        const int *drp = plan.counts + 2, *dri = drp + s_n + 1;
-        const float *drw = (const float *)(dri + total);
-        prof.mark(COLI_HIP_K_COMBINE);
-        launch_combine((float *)c->red_out.p, s.y, drp, dri, drw, s_n, D, s.ys, c->stream);
-        res = (float *)c->red_out.p;
+    // x ([total][D] f32) is staged in the y buffer, which has exactly that
+    // shape: the x quantisation reads it before the down projection writes y.
+    float *x_dev = (float *)c->y.p;
+    float *res = red ? (float *)c->red_out.p : s.y;
+
+    // The whole call as stream work: contents in, kernels, result out. The
+    // same sequence runs eagerly or is captured once per shape.
+    const bool profile = profiling() != 0;
+    auto enqueue = [&](Prof &prof, bool phases) -> int {
+        if (phases) hipEventRecord(c->phase_ev[0], c->stream);
+        if (!hip_ok(hipMemcpyAsync(dm, hm, meta_b, hipMemcpyHostToDevice, c->stream), "expert group metadata") ||
+            !hip_ok(hipMemcpyAsync(x_dev, c->pin_x.p, xb, hipMemcpyHostToDevice, c->stream),
+                    "expert group input upload"))
+            return 0;
+        if (phases) hipEventRecord(c->phase_ev[1], c->stream);
+        prof.mark(-1);
+        run_experts(c, prof, (const ExpertDesc *)dm, plan, gg, gd, x_dev, total, true, total, T, ga, arm, s, opt);
+        if (red) {
+            const int *drp = plan.counts + 2, *dri = drp + s_n + 1;
+            const float *drw = (const float *)(dri + total);
+            prof.mark(COLI_HIP_K_COMBINE);
+            launch_combine((float *)c->red_out.p, s.y, drp, dri, drw, s_n, D, s.ys, c->stream);
+        }
+        prof.mark(-1);
+        if (phases) hipEventRecord(c->phase_ev[2], c->stream);
+        if (!hip_ok(hipGetLastError(), "expert group launch") ||
+            !hip_ok(hipMemcpyAsync(c->pin_y.p, res, ob, hipMemcpyDeviceToHost, c->stream),
+                    "expert group output download"))
+            return 0;
+        if (phases) hipEventRecord(c->phase_ev[3], c->stream);
+        return 1;
+    };
+    auto finish = [&]() -> int {
+        if (!check_waits(c)) return 0;
+        std::memcpy(red ? red->out : y, c->pin_y.p, ob);
+        note_group(count, total);
+        return 1;
+    };
+
+    const bool graphs_on = graph_cache_enabled();
+    if (graphs_on && !profile && !g_dbg_gu && !g_dbg_dn) {
+        const ColiHipTensor *g0 = gates[0], *d0 = downs[0];
+        const ShapeKey key = shape_key({arm, count, D, gg.O, s_n, ga, g0->fmt, g0->gs, d0->fmt, d0->gs, g_spin_limit},
+                                       rows, count);
+        ColiHipGraph *g = graph_lookup(c, key);
+        if (!g) {
+            Prof off(c);
+            off.on = false;
+            int ok = hip_ok(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "graph begin capture");
+            ok = ok && enqueue(off, false);
+            hipGraph_t graph = nullptr;
+            const hipError_t end = hipStreamEndCapture(c->stream, &graph);   // always ends a begun capture
+            hipGraphExec_t exec = nullptr;
+            ok = ok && hip_ok(end, "graph end capture") &&
+                 hip_ok(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "graph instantiate");
+            if (ok) g = (ColiHipGraph *)std::calloc(1, sizeof(ColiHipGraph));
+            if (!g) {
+                // a failed capture: nothing recorded near it is trusted again
+                if (exec) hipGraphExecDestroy(exec);
+                if (graph) hipGraphDestroy(graph);
+                graph_cache_clear(c);
+                (void)hipGetLastError();
+                return fail("expert group: graph capture failed; the device's graph cache was cleared");
+            }
+            g->graph = graph;
+            g->exec = exec;
+            g->device = device;
+            g->gen = c->gen;
+            graph_store(c, key, g);
+            std::lock_guard<std::mutex> lock(g_stats_mu);
+            g_graph_captures++;
+        } else {
+            std::lock_guard<std::mutex> lock(g_stats_mu);
+            g_graph_replays++;
+        }
+        if (!hip_ok(hipGraphLaunch(g->exec, c->stream), "expert group graph launch") ||
+            !hip_ok(hipStreamSynchronize(c->stream), "expert group graph synchronize"))
+            return 0;
+        return finish();
     }
-    prof.mark(-1);
-    if (!hip_ok(hipGetLastError(), "expert group launch") ||
-        !hip_ok(hipMemcpyAsync(c->pin_y.p, res, ob, hipMemcpyDeviceToHost, c->stream), "expert group output download") ||
-        !hip_ok(hipStreamSynchronize(c->stream), "expert group synchronize"))
-        return 0;
+    if (graphs_on) {
+        std::lock_guard<std::mutex> lock(g_stats_mu);
+        g_graph_uncacheable++;
+    }
+
+    Prof prof(c);
+    bool phases = profile;
+    for (auto &e : c->phase_ev)
+        if (phases && !e && hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) phases = false;
+    if (!enqueue(prof, phases) || !hip_ok(hipStreamSynchronize(c->stream), "expert group synchronize")) return 0;
     prof.finish();
-    std::memcpy(red ? red->out : y, c->pin_y.p, ob);
-    note_group(count, total);
-    return 1;
+    if (phases) {
+        float h2d = 0, d2h = 0;
+        hipEventElapsedTime(&h2d, c->phase_ev[0], c->phase_ev[1]);
+        hipEventElapsedTime(&d2h, c->phase_ev[2], c->phase_ev[3]);
+        std::lock_guard<std::mutex> lock(g_stats_mu);
+        g_h2d_ms += h2d;
+        g_d2h_ms += d2h;
+    }
+    return finish();
 }
 
 }  // namespace
@@ -731,6 +945,15 @@ int coli_hip_init(const int *devices, int count) {
             g_nctx = 0;
             return 0;
         }
+        if (!hip_ok(hipHostMalloc((void **)&c->wait_flag, sizeof(int), hipHostMallocMapped | hipHostMallocCoherent),
+                    "wait flag allocation") ||
+            !hip_ok(hipHostGetDevicePointer((void **)&c->wait_flag_dev, c->wait_flag, 0), "wait flag mapping")) {
+            free_ctx(c);
+            for (int j = 0; j < g_nctx; j++) free_ctx(&g_ctx[j]);
+            g_nctx = 0;
+            return 0;
+        }
+        *c->wait_flag = 0;
         g_nctx++;
         int lds = 0;
         if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device) != hipSuccess) lds = 0;
@@ -891,15 +1114,10 @@ int coli_hip_graph_launch(ColiHipGraph *g) {
     if (!select_ctx(c)) return 0;
     if (c->gen != g->gen) return fail("graph launch: scratch was reallocated after the capture; capture the graph again");
     if (!hip_ok(hipGraphLaunch(g->exec, c->stream), "graph launch")) return 0;
-    return hip_ok(hipStreamSynchronize(c->stream), "graph synchronize");
+    return hip_ok(hipStreamSynchronize(c->stream), "graph synchronize") && check_waits(c);
 }
 
-void coli_hip_graph_free(ColiHipGraph *g) {
-    if (!g) return;
-    if (g->exec) hipGraphExecDestroy(g->exec);
-    if (g->graph) hipGraphDestroy(g->graph);
-    std::free(g);
-}
+void coli_hip_graph_free(ColiHipGraph *g) { graph_destroy(g); }
 
 void coli_hip_graph_cache_stats(uint64_t *captures, uint64_t *replays, uint64_t *invalidations,
                                 uint64_t *uncacheable) {
@@ -913,7 +1131,7 @@ void coli_hip_graph_cache_stats(uint64_t *captures, uint64_t *replays, uint64_t 
 int coli_hip_pipe_sync(int device) {
     Ctx *c = find_ctx(device);
     if (!select_ctx(c)) return 0;
-    return hip_ok(hipStreamSynchronize(c->stream), "stream synchronize");
+    return hip_ok(hipStreamSynchronize(c->stream), "stream synchronize") && check_waits(c);
 }
 
 void *coli_hip_pipe_alloc(int device, size_t bytes) {
@@ -1012,19 +1230,16 @@ void coli_hip_kernel_stats(int which, uint64_t *launches, double *total_ms) {
 void coli_hip_reset_stats(void) {
     std::lock_guard<std::mutex> lock(g_stats_mu);
     g_calls = g_experts = g_rows = 0;
-    g_h2d_ms = g_kernel_ms = g_d2h_ms = 0;
+    g_h2d_ms = g_d2h_ms = 0;
     for (int i = 0; i < COLI_HIP_K_COUNT; i++) {
         g_k_launches[i] = 0;
         g_k_ms[i] = 0;
     }
 }
 
-int coli_hip_set_debug_trace(long long *gateup_dev, long long *down_dev) {
-    g_trace_gu = gateup_dev;
-    g_trace_dn = down_dev;
-#ifdef PHIP_GEMV_TRACE
-    phip::set_misc_trace(gateup_dev ? gateup_dev + 400000 : nullptr);
-#endif
+int coli_hip_set_spin_limit(int polls) {
+    if (polls < 0) return fail("spin limit must be >= 0");
+    g_spin_limit = polls ? polls : GEMV_SPIN_LIMIT;
     return 1;
 }
 

@@ -445,6 +445,12 @@ def set_debug_dots(gateup_ptr: int = 0, down_ptr: int = 0) -> None:
     lib.coli_hip_set_debug_dots(C.c_void_p(gateup_ptr or None), C.c_void_p(down_ptr or None))
 
 
+def set_spin_limit(polls: int) -> None:
+    """Test hook: polls before a GEMV bounded wait gives up (0: the default)."""
+    if lib.coli_hip_set_spin_limit(polls) != 1:
+        raise HipError("spin limit must be >= 0")
+
+
 def last_table(device, E, R):
     hdr = np.zeros(4, np.int32)
     uexp = np.zeros(E, np.int32)

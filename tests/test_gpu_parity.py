@@ -746,3 +746,72 @@ def test_limits_512_experts_top16(hip, orc, S, arm):
     bl2 = hip.DeviceBuffer.from_array(synth.normal_logits(rng, S, E + 1))
     with pytest.raises(hip.HipError):
         hip.moe_forward_logits_dev(big, bx.ptr, S, bl2.ptr, k, bids.ptr, bw.ptr, bout.ptr, 32, arm)
+
+
+# ------------------------------------------------------------ BASELINE configs 1 and 5 at size
+
+@pytest.mark.parametrize("ga", [32, 0])
+def test_single_expert_fused_down_combine_full_shape(hip, orc, ga):
+    """one expert, one token, D=5120, I=1536, k=1. The down
+    projection runs gemv_down_combine_kernel at its widest K (48 blocks =
+    DC_MAXNB); bit-identical to the oracle (matmul.rs:93-106, mlp.rs:21-26)."""
+    say("config 1 full shape", ga)
+    rng = np.random.default_rng(5120 + ga)
+    E, D, I, S, k = 1, 5120, 1536, 1, 1
+    gpu, ora, eset, x, logits = _layer_case(hip, orc, rng, E, D, I, S, k)
+    bx, bl = hip.DeviceBuffer.from_array(x), hip.DeviceBuffer.from_array(logits)
+    bids, bw, bout = hip.DeviceBuffer(4), hip.DeviceBuffer(4), hip.DeviceBuffer(D * 4)
+    for mode in (-1, 0):   # automatic (k = 1: fused) and the separate down + combine
+        hip.set_fused_combine(mode)
+        try:
+            hip.moe_forward_logits_dev(eset, bx.ptr, 1, bl.ptr, k, bids.ptr, bw.ptr, bout.ptr, ga)
+            hip.pipe_sync(0)
+        finally:
+            hip.set_fused_combine(-1)
+        ids, w = bids.download(np.int32, (1, 1)), bw.download(np.float32, (1, 1))
+        assert ids[0, 0] == 0 and w[0, 0] == 1.0
+        out = bout.download(np.float32, (1, D))
+        ref = orc.moe_forward(x, ids, w, ora, ga)
+        assert np.array_equal(out, ref), (mode, nerr(out, ref))
+
+
+def _cfg5_case(hip, orc, fmt, seed, n_dist=16):
+    """BASELINE config 5 shape: D=6144, I=2048, 256 experts, 512 tokens,
+    uniform top-8. The 256 expert slots alias n_dist distinct uploaded experts
+    (device memory and host oracle time), so the dispatch has config 5's
+    table, tile count and kernel instantiations (about 16 rows per expert:
+    non-temporal weight copies)."""
+    rng = np.random.default_rng(seed)
+    E, D, I, S = 256, 6144, 2048, 512
+    gpu, ora = _experts(rng, n_dist, D, I, fmt, 32, orc, hip)
+    eset = hip.ExpertSet([gpu[e % n_dist] for e in range(E)])
+    ora_full = [ora[e % n_dist] for e in range(E)]
+    x = rng.standard_normal((S, D)).astype(np.float32)
+    logits = synth.normal_logits(rng, S, E)
+    return gpu, ora_full, eset, x, logits
+
+
+@pytest.mark.parametrize("fmt", [qt.FMT_I4G, qt.FMT_I8G])
+def test_large_layer_cfg5_sampled(hip, orc, fmt):
+    """Config 5 through both device-resident entry points (router fused with
+    the activation quant, then precomputed ids as the bench's later layers),
+    int4 and int8 weights, sampled tokens bit-identical to the oracle
+    (matmul.rs:61-72 int8, idot.rs:98-110 grouped)."""
+    say("config 5", fmt)
+    gpu, ora, eset, x, logits = _cfg5_case(hip, orc, fmt, 6144 + fmt)
+    S, D, E, k = 512, 6144, 256, 8
+    bx, bl = hip.DeviceBuffer.from_array(x), hip.DeviceBuffer.from_array(logits)
+    bids, bw = hip.DeviceBuffer(S * k * 4), hip.DeviceBuffer(S * k * 4)
+    b1, b2 = hip.DeviceBuffer(S * D * 4), hip.DeviceBuffer(S * D * 4)
+    hip.moe_forward_logits_dev(eset, bx.ptr, S, bl.ptr, k, bids.ptr, bw.ptr, b1.ptr, 32)
+    hip.moe_forward_dev(eset, bx.ptr, S, bids.ptr, bw.ptr, k, b2.ptr, 32)
+    hip.pipe_sync(0)
+    ids, w = bids.download(np.int32, (S, k)), bw.download(np.float32, (S, k))
+    ri, rw = orc.route_softmax_topk(logits, k)
+    assert np.array_equal(ids, ri) and np.array_equal(w, rw)
+    o1, o2 = b1.download(np.float32, (S, D)), b2.download(np.float32, (S, D))
+    assert np.array_equal(o1, o2)
+    sub = np.array([0, 1, 130, 257, 400, 511])
+    ref = orc.moe_forward(x, ids, w, ora, 32, subset=sub, nthreads=8)
+    assert np.array_equal(o1[sub], ref[sub]), nerr(o1[sub], ref[sub])
+    assert np.all(np.isfinite(o1))
