@@ -170,6 +170,19 @@ int coli_hip_route_sigmoid_topk_dev(int device, const float *logits_dev, const f
  * Async on the device stream (coli_hip_pipe_sync waits). */
 int coli_hip_moe_forward_dev(const ColiHipExpertSet *set, const float *x_dev, int S, const int *ids_dev,
                              const float *w_dev, int k, float *out_dev, int act_group, int arm);
+/* The same layer as coli_hip_moe_forward_dev, allocating nothing: no
+ * hipMalloc, hipFree or other allocating call, so callers that cannot
+ * allocate (code under stream/graph capture, tight serving loops, harnesses
+ * that forbid it) can use it from the first call. No counterpart in the
+ * reference. Its scratch (activation quant, h, y, the expert-offset table) is
+ * a fixed COLI_HIP_FIXED_SCRATCH_BYTES array per device, mapped at init; a
+ * call needing more returns 0 with a message (about S * k <= 2300 rows at
+ * D = 5120, I = 1536). Every call on a device shares that device's array and
+ * leaves its contents behind: calls that overlap on one device (other host
+ * threads, other streams) race. No profiling on this path. */
+#define COLI_HIP_FIXED_SCRATCH_BYTES (64 << 20)
+int coli_hip_moe_forward_dev_noalloc(const ColiHipExpertSet *set, const float *x_dev, int S, const int *ids_dev,
+                                     const float *w_dev, int k, float *out_dev, int act_group, int arm);
 /* Same layer with the router fused in: logits[S][E] (device) are routed
  * (as coli_hip_route_softmax_topk_dev) into ids_dev/w_dev [S][k], then the
  * layer runs. One token (S = 1) on the GEMV arm needs no expert table. */

@@ -69,6 +69,7 @@ SIGNATURES = {
     "coli_hip_route_softmax_topk_dev": (_i, [_i, _p, _i, _i, _i, _p, _p]),
     "coli_hip_route_sigmoid_topk_dev": (_i, [_i, _p, _p, _i, _i, _i, _i, C.c_float, C.c_float, _p, _p, _p]),
     "coli_hip_moe_forward_dev": (_i, [_p, _p, _i, _p, _p, _i, _p, _i, _i]),
+    "coli_hip_moe_forward_dev_noalloc": (_i, [_p, _p, _i, _p, _p, _i, _p, _i, _i]),
     "coli_hip_moe_forward_logits_dev": (_i, [_p, _p, _i, _p, _i, _p, _p, _p, _i, _i]),
     "coli_hip_stream": (_p, [_i]),
     "coli_hip_set_profile": (_i, [_i]),

@@ -18,6 +18,12 @@
 
 using namespace phip;
 
+// Scratch of coli_hip_moe_forward_dev_noalloc: a fixed array in every
+// device's code object, mapped at init (hipGetSymbolAddress per device).
+// Host code uses only the per-device address kept in Ctx::fixed_scratch,
+// never this name.
+static __device__ __align__(256) uint8_t scratch[COLI_HIP_FIXED_SCRATCH_BYTES];
+
 namespace {
 struct Slab;
 }
@@ -79,6 +85,9 @@ struct Ctx {
     int *wait_flag = nullptr, *wait_flag_dev = nullptr;
     GraphSlot graphs[GRAPH_CACHE];
     uint64_t graph_clock = 0;
+    // device address of this device's copy of the fixed scratch array (the
+    // no-allocation entry point), looked up at init with the device current
+    uint8_t *fixed_scratch = nullptr;
     // last device-resident table (for coli_hip_last_table)
     TableOut tbl_view{};
     int tbl_E = 0, tbl_R = 0;
@@ -551,6 +560,35 @@ int reserve_rows(Ctx *c, const MatGeom &gg, const MatGeom &gd, int rows_x, int R
     return 1;
 }
 
+// The same per-row scratch as reserve_rows, laid out from `base` (256-byte
+// aligned pieces). With base == nullptr only the size is computed.
+int carve_rows(const MatGeom &gg, const MatGeom &gd, int rows_x, int R, int ga, uint8_t *base, size_t *bytes,
+               Scratch *s) {
+    s->xs = gg.Kp;
+    s->sxs = ga == 32 ? gg.nb : 1;
+    s->hs = gd.Kp;
+    s->hqs = gd.Kp;
+    s->shs = ga == 32 ? gd.nb : 1;
+    s->ys = gd.O;
+    const size_t sz[6] = {(size_t)rows_x * s->xs, (size_t)rows_x * s->sxs * 4, (size_t)R * s->hs * 4,
+                          (size_t)R * s->hqs, (size_t)R * s->shs * 4, (size_t)R * s->ys * 4};
+    size_t off = 0, at[6];
+    for (int i = 0; i < 6; i++) {
+        at[i] = off;
+        off += round_up(std::max(sz[i], (size_t)1), 256);
+    }
+    *bytes = off;
+    if (base) {
+        s->xq = (int8_t *)(base + at[0]);
+        s->sx = (float *)(base + at[1]);
+        s->h = (float *)(base + at[2]);
+        s->hq = (int8_t *)(base + at[3]);
+        s->sh = (float *)(base + at[4]);
+        s->y = (float *)(base + at[5]);
+    }
+    return 1;
+}
+
 // Optional pieces of a dispatch beyond the expert matmuls.
 struct DispatchOpts {
     bool x_quantized = false;   // xq/sx already written (fused router + quant)
@@ -954,6 +992,12 @@ int coli_hip_init(const int *devices, int count) {
             return 0;
         }
         *c->wait_flag = 0;
+        if (!hip_ok(hipGetSymbolAddress((void **)&c->fixed_scratch, HIP_SYMBOL(scratch)), "fixed scratch mapping")) {
+            free_ctx(c);
+            for (int j = 0; j < g_nctx; j++) free_ctx(&g_ctx[j]);
+            g_nctx = 0;
+            return 0;
+        }
         g_nctx++;
         int lds = 0;
         if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device) != hipSuccess) lds = 0;
@@ -1317,7 +1361,7 @@ int coli_hip_route_softmax_topk_dev(int device, const float *logits_dev, int S, 
 namespace {
 
 int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, const float *logits_dev, int *ids_dev,
-                     float *w_dev, int k, float *out_dev, int ga, int arm) {
+                     float *w_dev, int k, float *out_dev, int ga, int arm, bool fixed_scratch = false) {
     if (!set || !x_dev || !ids_dev || !w_dev || !out_dev || S < 1 || k < 1) return 0;
     if (k > 16) return fail("moe_forward: k > 16 is not supported");
     if (set->count > 512) return fail("moe_forward: more than 512 experts");
@@ -1335,8 +1379,28 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
     const size_t n_int =
         4 + (size_t)E + (E + 1) + 3 * (size_t)R + 2 * (size_t)R + 3 * (size_t)tmax + table_work_ints(S, k, E);
     Scratch s{};
-    if (!reserve_rows(c, gg, gd, S, R, ga, &s) || !reserve(c, c->tbl, n_int * 4)) return 0;
-    int *p = (int *)c->tbl.p;
+    int *p = nullptr;
+    if (fixed_scratch) {
+        // the whole dispatch's scratch carved out of the device's fixed array:
+        // nothing is allocated, so sizes beyond it are refused
+        if (!c->fixed_scratch) return fail("moe_forward (no allocation): the fixed scratch array is not mapped");
+        size_t need = 0;
+        if (!carve_rows(gg, gd, S, R, ga, nullptr, &need, &s)) return 0;
+        const size_t tbl_off = need;
+        need += round_up(n_int * 4, 256);
+        if (need > COLI_HIP_FIXED_SCRATCH_BYTES) {
+            std::fprintf(stderr,
+                         "[HIP] moe_forward (no allocation): this call needs %zu bytes of scratch, more than the "
+                         "fixed %d MiB\n",
+                         need, COLI_HIP_FIXED_SCRATCH_BYTES >> 20);
+            return 0;
+        }
+        carve_rows(gg, gd, S, R, ga, c->fixed_scratch, &need, &s);
+        p = (int *)(c->fixed_scratch + tbl_off);
+    } else {
+        if (!reserve_rows(c, gg, gd, S, R, ga, &s) || !reserve(c, c->tbl, n_int * 4)) return 0;
+        p = (int *)c->tbl.p;
+    }
     TableOut t{};
     t.hdr = p;
     p += 4;
@@ -1366,6 +1430,7 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
     c->tbl_R = R;
 
     Prof prof(c);
+    if (fixed_scratch) prof.on = false;   // profiling creates events: not on the no-allocation path
     DispatchOpts opt;
     opt.w_reuse = R >= 2 * MT_ROWS * E;   // about two or more M tiles per expert
     const int act = epi_act(ga);
@@ -1443,6 +1508,11 @@ extern "C" {
 int coli_hip_moe_forward_dev(const ColiHipExpertSet *set, const float *x_dev, int S, const int *ids_dev,
                              const float *w_dev, int k, float *out_dev, int ga, int arm) {
     return moe_forward_impl(set, x_dev, S, nullptr, (int *)ids_dev, (float *)w_dev, k, out_dev, ga, arm);
+}
+
+int coli_hip_moe_forward_dev_noalloc(const ColiHipExpertSet *set, const float *x_dev, int S, const int *ids_dev,
+                                     const float *w_dev, int k, float *out_dev, int ga, int arm) {
+    return moe_forward_impl(set, x_dev, S, nullptr, (int *)ids_dev, (float *)w_dev, k, out_dev, ga, arm, true);
 }
 
 int coli_hip_moe_forward_logits_dev(const ColiHipExpertSet *set, const float *x_dev, int S, const float *logits_dev,

@@ -408,6 +408,14 @@ def moe_forward_dev(eset: ExpertSet, x_ptr, S, ids_ptr, w_ptr, k, out_ptr, act_g
         raise HipError("hip moe_forward failed")
 
 
+def moe_forward_dev_noalloc(eset: ExpertSet, x_ptr, S, ids_ptr, w_ptr, k, out_ptr, act_group=0, arm=ARM_AUTO):
+    """As moe_forward_dev, with no device allocation: scratch is the device's
+    fixed array (refused above its size)."""
+    if lib.coli_hip_moe_forward_dev_noalloc(eset.ptr, C.c_void_p(x_ptr), S, C.c_void_p(ids_ptr),
+                                            C.c_void_p(w_ptr), k, C.c_void_p(out_ptr), act_group, arm) != 1:
+        raise HipError("hip moe_forward (no allocation) failed")
+
+
 def moe_forward_logits_dev(eset: ExpertSet, x_ptr, S, logits_ptr, k, ids_ptr, w_ptr, out_ptr, act_group=0,
                            arm=ARM_AUTO):
     """Async: route logits[S][E] (writing ids/w) and run the layer, router fused."""
