@@ -514,6 +514,7 @@ static void launch_dc(const DotArgs &a, const MatGeom &g, int k, const float *w,
 void launch_gemv_down_combine(const DotArgs &a, const MatGeom &g, int act, int k, const float *w, float *out,
                               hipStream_t st) {
     const int epi = act == ACT_B32 ? EPI_B32 : (g.per_row ? EPI_ROW : EPI_GRP);
+
     if (g.w4) {
         if (epi == EPI_ROW) launch_dc<true, EPI_ROW>(a, g, k, w, out, st);
         else if (epi == EPI_GRP) launch_dc<true, EPI_GRP>(a, g, k, w, out, st);

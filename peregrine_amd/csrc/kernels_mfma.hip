@@ -562,6 +562,314 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATEUP || !
     }
 }
 
+// ---------------------------------------------------------------------------
+// Scalar-address staged variant. The same stages and per-block barrier as
+// mfma_dma_kernel, with two changes that take the per-block address work off
+// the VALU (which the exact f32 epilogue already keeps busy):
+//  * every LDS-DMA copy uses the scalar-base form: a uniform 64-bit base in
+//    SGPRs, advanced per block by scalar adds, plus a fixed 32-bit per-lane
+//    offset. For that, each copy reads one tensor: wave w copies subtiles 2w
+//    and 2w+1 of the stage (gate/up: waves 0-1 the gate tiles of channel
+//    groups 0-3, waves 2-3 the up tiles; down: its own two subtiles);
+//  * the block loop is unrolled over the stages, so every LDS offset is an
+//    instruction immediate.
+// Stage: [A: 32 rows x 32 B][8 weight subtiles x 32 x BB][8 x 32 f32 scales].
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void lds_dma16_s(uint32_t voff, const void *base, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "memory");
+}
+__device__ __forceinline__ void lds_dma16_s_nt(uint32_t voff, const void *base, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(base), "s"(lds) : "memory");
+}
+__device__ __forceinline__ void lds_dma4_s(uint32_t voff, const void *base, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "memory");
+}
+__device__ __forceinline__ const uint8_t *uniform_ptr(const void *p) {
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const uint8_t *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+template <bool W4>
+struct SaStage {
+    static constexpr int SUB = 32 * (W4 ? 16 : 32);   // one 32-column subtile of one block
+    static constexpr int A = 0;
+    static constexpr int W = 1024;
+    static constexpr int S = W + 8 * SUB;
+    static constexpr int BYTES = S + 8 * 128;
+};
+
+template <bool W4, int EPI, bool GATEUP, int PD, bool WNT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATEUP || !W4 ? 1 : 4))) void mfma_sa_kernel(DotArgs a, MatGeom g) {
+    constexpr int NSUB = 2;
+    typedef SaStage<W4> ST;
+    constexpr int NSTG = PD + 2;   // stage b-2 is refilled once every wave is past block b-1's barrier
+    constexpr int NU = NSTG % 2 ? 2 * NSTG : NSTG;   // unroll: stages and the two result buffers rotate
+    constexpr int OPS = 1 + (W4 ? 1 : 2) + (EPI != EPI_ROW ? 1 : 0);   // copies per block and wave
+    constexpr int BB = W4 ? 16 : 32;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds_u8[];   // [NSTG][ST::BYTES], then sxl
+
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int tile = blockIdx.y;
+    if (tile >= a.plan.counts[1]) return;
+    const int e = a.plan.mt_exp[tile], r0 = a.plan.mt_row0[tile], rend = a.plan.mt_rend[tile];
+    const int j = lane & 31, hh = lane >> 5;
+    const int n0 = GATEUP ? ((int)blockIdx.x * 4 + wave) * 32 : ((int)blockIdx.x * 4 + wave) * 32 * NSUB;
+    const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_u8);
+    float *sxl = (float *)(lds_u8 + (size_t)NSTG * ST::BYTES);   // EPI_B32: [nb][32] activation scales
+    auto act_row = [&](int r) { return a.act_identity ? r : a.plan.row_act[r]; };
+
+    // ---- copy sources: uniform bases + per-lane offsets ----
+    // A: a dword of row 8*wave + lane/8 (rows past the expert's end repeat
+    // its last row; never stored)
+    int ra = r0 + 8 * wave + (lane >> 3);
+    if (ra >= rend) ra = rend - 1;
+    const uint32_t voff_a = (uint32_t)act_row(ra) * (uint32_t)a.x_stride + (uint32_t)(lane & 7) * 4;
+    const uint8_t *base_a = uniform_ptr(a.xq);
+    // weights and their scales: this wave's two subtiles 2w, 2w+1 (one
+    // tensor), lane half hh -> subtile 2w + hh; tiles past the tensor clamp
+    // to its last tile (never stored)
+    const int mat = GATEUP ? (wave >> 1) : 2;
+    const int ntile = g.Op / TILE_O;
+    int wt = GATEUP ? (int)blockIdx.x * 4 + 2 * (wave & 1) + hh : (int)blockIdx.x * 8 + 2 * wave + hh;
+    if (wt >= ntile) wt = ntile - 1;
+    const uint8_t *base_w = uniform_ptr(a.desc[e].w[mat]);
+    const uint8_t *base_s = uniform_ptr(a.desc[e].sc[mat]);
+    const uint32_t tile_w = (uint32_t)g.nb * ST::SUB;
+    uint32_t voff_w;
+    if constexpr (W4) voff_w = (uint32_t)wt * tile_w + (uint32_t)j * 16;
+    else voff_w = (uint32_t)(lane >> 1) * 32 + (uint32_t)(lane & 1) * 16;   // int8: one subtile per copy
+    uint32_t tile_w8[2] = {0, 0};
+    if constexpr (!W4) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            int t = GATEUP ? (int)blockIdx.x * 4 + 2 * (wave & 1) + q : (int)blockIdx.x * 8 + 2 * wave + q;
+            if (t >= ntile) t = ntile - 1;
+            tile_w8[q] = __builtin_amdgcn_readfirstlane((uint32_t)t * tile_w);
+        }
+    }
+    const uint32_t voff_s = (uint32_t)wt * (uint32_t)g.ng * 128 + (uint32_t)j * 4;
+
+    auto copy_blk = [&](int b, int stg) {
+        const uint32_t st = lds_addr + (uint32_t)(stg * ST::BYTES);
+        lds_dma4_s(voff_a, base_a + (size_t)b * BLK, st + ST::A + wave * 256);
+        const uint8_t *wb = base_w + (size_t)b * ST::SUB;
+        if constexpr (W4) {
+            if constexpr (WNT) lds_dma16_s_nt(voff_w, wb, st + ST::W + wave * 2 * ST::SUB);
+            else lds_dma16_s(voff_w, wb, st + ST::W + wave * 2 * ST::SUB);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                if constexpr (WNT) lds_dma16_s_nt(voff_w, wb + tile_w8[q], st + ST::W + (wave * 2 + q) * ST::SUB);
+                else lds_dma16_s(voff_w, wb + tile_w8[q], st + ST::W + (wave * 2 + q) * ST::SUB);
+            }
+        }
+        if constexpr (EPI != EPI_ROW)
+            lds_dma4_s(voff_s, base_s + (size_t)grp_of(b, g.gshift) * 128, st + ST::S + wave * 256);
+    };
+
+    // the tile's activation scales ([nb][32] in LDS), all issued at once:
+    // one copy per wave covers two blocks of the 32 rows; block 0's wait
+    // covers them (a wave's loads complete in order)
+    if constexpr (EPI == EPI_B32) {
+        int rx = r0 + (lane & 31);
+        if (rx >= rend) rx = rend - 1;
+        const float *srcx = a.sx + (size_t)act_row(rx) * a.sx_stride;
+        const uint32_t sx_lds = lds_addr + (uint32_t)(NSTG * ST::BYTES);
+        for (int i = wave; i < (g.nb + 1) >> 1; i += 4) {
+            const int b = min(2 * i + (lane >> 5), g.nb - 1);
+            lds_dma4(srcx + b, sx_lds + (uint32_t)(i * 256));
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < PD; ++u)
+        if (u < g.nb) copy_blk(u, u);
+
+    int oc[NSUB];
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) oc[s] = GATEUP ? n0 + j : n0 + s * 32 + j;
+    // this wave's subtiles in the stage: gate/up -> gate group w and up group
+    // w; down -> subtiles 2w, 2w+1
+    const int sub0 = GATEUP ? wave : 2 * wave, sub1 = GATEUP ? 4 + wave : 2 * wave + 1;
+    const uint32_t rd_w0 = ST::W + sub0 * ST::SUB + j * BB + hh * (BB / 2);
+    const uint32_t rd_w1 = ST::W + sub1 * ST::SUB + j * BB + hh * (BB / 2);
+    const uint32_t rd_s0 = ST::S + sub0 * 128 + j * 4, rd_s1 = ST::S + sub1 * 128 + j * 4;
+    const uint32_t rd_a = ST::A + j * 32 + hh * 16;
+    float acc[NSUB][16];
+    v16i iacc[NSUB];
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[s][i] = 0.0f;
+        iacc[s] = v16i{};
+    }
+    const int nrow = rend - r0;
+
+    auto read_ops = [&](int stg, v4i &A, v4i (&B)[NSUB], float (&S)[NSUB]) {
+        const uint8_t *st = lds_u8 + stg * ST::BYTES;
+        A = *(const v4i *)(st + rd_a);
+        const uint32_t rw[2] = {rd_w0, rd_w1}, rs[2] = {rd_s0, rd_s1};
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) {
+            if constexpr (W4) {
+                const uint2 w = *(const uint2 *)(st + rw[s]);
+                B[s][0] = i4_even16(w.x);
+                B[s][1] = i4_odd16(w.x);
+                B[s][2] = i4_even16(w.y);
+                B[s][3] = i4_odd16(w.y);
+            } else {
+                B[s] = *(const v4i *)(st + rw[s]);
+            }
+            if constexpr (EPI != EPI_ROW) S[s] = *(const float *)(st + rs[s]);
+        }
+    };
+    auto mma_blk = [&](int b, const v4i &A, const v4i (&B)[NSUB], v16i (&D)[NSUB]) {
+        const bool opens = EPI == EPI_B32 || (EPI == EPI_GRP && (b == 0 || grp_end(b - 1, g.gshift, g.nb))) ||
+                           (EPI == EPI_ROW && b == 0);
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) {
+            const v16i cin = opens ? v16i{} : iacc[s];
+            D[s] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B[s], cin, 0, 0, 0);
+            if (EPI != EPI_B32) iacc[s] = D[s];
+        }
+    };
+    auto epi_blk = [&](int b, const v16i (&D)[NSUB], const float (&S)[NSUB]) {
+        if constexpr (EPI == EPI_ROW) return;
+        if (EPI == EPI_GRP && !grp_end(b, g.gshift, g.nb)) return;
+        if constexpr (EPI == EPI_B32) {
+            const float4 *sx4 = (const float4 *)(sxl + b * 32 + 4 * hh);
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+                if (8 * gq >= nrow) break;   // uniform: rows past the tile's end
+                const float4 sq = sx4[2 * gq];
+                const float sxr[4] = {sq.x, sq.y, sq.z, sq.w};
+#pragma unroll
+                for (int s = 0; s < NSUB; ++s) {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const int i = 4 * gq + t;
+                        acc[s][i] = __fmaf_rn(__fmul_rn(S[s], sxr[t]), (float)D[s][i], acc[s][i]);
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+                if (8 * gq >= nrow) break;
+#pragma unroll
+                for (int s = 0; s < NSUB; ++s) {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const int i = 4 * gq + t;
+                        acc[s][i] = __fadd_rn(acc[s][i], __fmul_rn((float)D[s][i], S[s]));
+                    }
+                }
+            }
+        }
+    };
+
+    v16i Dr[2][NSUB];
+    float Sr[2][NSUB];
+#pragma unroll 1
+    for (int b0 = 0; b0 < g.nb; b0 += NU) {
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+            const int bb = b0 + u;   // stage u % NSTG: b0 is a multiple of NSTG
+            if (bb < g.nb) {   // uniform
+                if (bb + PD < g.nb) {
+                    copy_blk(bb + PD, (u + PD) % NSTG);
+                    wait_vm<OPS * PD>();   // this wave's copies of block bb have landed
+                } else {
+                    wait_vm<0>();          // the last blocks: nothing copied past the end
+                }
+                asm volatile("s_barrier" ::: "memory");
+                v4i A;
+                v4i B[NSUB];
+                read_ops(u % NSTG, A, B, Sr[u & 1]);
+                mma_blk(bb, A, B, Dr[u & 1]);
+            }
+            if (bb > 0 && bb - 1 < g.nb) epi_blk(bb - 1, Dr[(u + 1) & 1], Sr[(u + 1) & 1]);
+        }
+    }
+    if (g.nb % NU == 0) epi_blk(g.nb - 1, Dr[1], Sr[1]);   // the last block's epilogue did not run in the loop
+
+    // per-row activation scale (EPI_ROW / EPI_GRP) of each accumulator row
+    float v[NSUB][16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        float sxr = 1.0f;
+        if constexpr (EPI != EPI_B32) {
+            int rr = r0 + acc_row(i, lane);
+            if (rr >= rend) rr = rend - 1;
+            sxr = a.sx[(size_t)act_row(rr) * a.sx_stride];
+        }
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) {
+            if constexpr (EPI == EPI_ROW) {
+                const int D = W4 ? (iacc[s][i] >> 4) : iacc[s][i];
+                int o = oc[s];
+                if (o >= g.Op) o = g.Op - 1;
+                const int m = GATEUP ? s : 2;
+                const float *sp = a.desc[e].sc[m] + (size_t)(o / TILE_O) * g.ng * TILE_O + (o % TILE_O);
+                const float sc = W4 ? __fmul_rn(sp[0], 16.0f) : sp[0];
+                v[s][i] = __fmul_rn(__fmul_rn((float)D, sc), sxr);
+            } else if constexpr (EPI == EPI_GRP) {
+                v[s][i] = __fmul_rn(acc[s][i], sxr);
+            } else {
+                v[s][i] = acc[s][i];
+            }
+        }
+    }
+
+    if constexpr (GATEUP) {
+        const int o = oc[0];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int row = r0 + acc_row(i, lane);
+            const float h = silu_mul(v[0][i], v[1][i]);
+            const bool ok = row < rend && o < ((g.O + 31) & ~31);
+            if (ok) a.out[(size_t)row * a.out_stride + o] = h;
+            if (EPI == EPI_B32 && a.hq) {
+                const float m = warp_max(fabsf(h), 32);
+                float sc = __fdiv_rn(m, 127.0f);
+                if (sc < 1e-12f) sc = 1e-12f;
+                const float inv = __fdiv_rn(1.0f, sc);
+                if (ok) {
+                    a.hq[(size_t)row * a.hq_stride + perm8(o)] = (int8_t)(int)rintf(__fmul_rn(h, inv));
+                    if (j == 0) a.sh[(size_t)row * a.sh_stride + (o >> 5)] = sc;
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) {
+            const int o = oc[s];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int row = r0 + acc_row(i, lane);
+                if (row < rend && o < g.O) a.out[(size_t)row * a.out_stride + o] = v[s][i];
+            }
+        }
+    }
+}
+
+template <bool W4, int EPI, int PD>
+static size_t mfma_sa_lds(const MatGeom &g) {
+    return (size_t)(PD + 2) * SaStage<W4>::BYTES + (EPI == EPI_B32 ? (size_t)(g.nb + 1) / 2 * 2 * 32 * sizeof(float) : 0);
+}
+
+template <bool W4, int EPI, bool GATEUP, int PD, bool WNT>
+static void launch_mfma_sa_h(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
+    const int ch_per_wg = GATEUP ? 4 * 32 : 4 * 32 * 2;
+    const int span = GATEUP ? ((g.O + 31) & ~31) : g.O;
+    dim3 grid((unsigned)((span + ch_per_wg - 1) / ch_per_wg), (unsigned)grid_tiles);
+    const size_t lds = mfma_sa_lds<W4, EPI, PD>(g);
+    auto kern = mfma_sa_kernel<W4, EPI, GATEUP, PD, WNT>;
+    static size_t opted[LDS_OPT_DEVICES];
+    lds_opt_in((const void *)kern, lds, opted);
+    launch_k(kern, grid, dim3(256), lds, st, a, g);
+}
+
 template <bool W4, int EPI, bool GATEUP, int PD>
 static void launch_mfma_p(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
     constexpr int NSUB = 2;
@@ -605,6 +913,16 @@ static void launch_mfma_dma_h(const DotArgs &a, const MatGeom &g, int grid_tiles
 // 4-7% slower cacheable.
 template <bool W4, int EPI, bool GATEUP, int PD>
 static void launch_mfma_dma(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
+    // int4 gate/up: the scalar-address kernel (config 4 1203 -> 1060 us,
+    // config 5 780 -> 766 us, config 3 209 -> 201 us). The down projections
+    // keep mfma_dma_kernel: capped at 128 VGPRs the unrolled loop spills
+    // (int4 down, config 4: 507 vs 759 us); int8 gate/up measured 1190 vs
+    // 1213 us (config 5).
+    if constexpr (W4 && GATEUP) {
+        if (a.w_reuse) launch_mfma_sa_h<W4, EPI, GATEUP, PD, false>(a, g, grid_tiles, st);
+        else launch_mfma_sa_h<W4, EPI, GATEUP, PD, true>(a, g, grid_tiles, st);
+        return;
+    }
     if (a.w_reuse) launch_mfma_dma_h<W4, EPI, GATEUP, PD, false>(a, g, grid_tiles, st);
     else launch_mfma_dma_h<W4, EPI, GATEUP, PD, true>(a, g, grid_tiles, st);
 }

@@ -504,8 +504,8 @@ struct Prof {
             if (!e && hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) on = false;
     }
     ~Prof() { g_launch_timing = LaunchTiming{}; }
-    void close_slot() {
-        if (n > 0) used[n - 1] = g_launch_timing.used;
+    void close_slot() {   // records whether the armed slot launched anything, then disarms
+        if (n > 0 && g_launch_timing.stop) used[n - 1] = g_launch_timing.used;
         g_launch_timing = LaunchTiming{};
     }
     void mark(int w) {   // the launches that follow belong to kernel slot w (w = -1: none)
