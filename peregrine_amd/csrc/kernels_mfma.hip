@@ -600,7 +600,7 @@ struct SaStage {
 };
 
 template <bool W4, int EPI, bool GATEUP, int PD, bool WNT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATEUP || !W4 ? 1 : 4))) void mfma_sa_kernel(DotArgs a, MatGeom g) {
+__global__ __launch_bounds__(256) void mfma_sa_kernel(DotArgs a, MatGeom g) {
     constexpr int NSUB = 2;
     typedef SaStage<W4> ST;
     constexpr int NSTG = PD + 2;   // stage b-2 is refilled once every wave is past block b-1's barrier
@@ -913,12 +913,12 @@ static void launch_mfma_dma_h(const DotArgs &a, const MatGeom &g, int grid_tiles
 // 4-7% slower cacheable.
 template <bool W4, int EPI, bool GATEUP, int PD>
 static void launch_mfma_dma(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
-    // int4 gate/up: the scalar-address kernel (config 4 1203 -> 1060 us,
-    // config 5 780 -> 766 us, config 3 209 -> 201 us). The down projections
-    // keep mfma_dma_kernel: capped at 128 VGPRs the unrolled loop spills
-    // (int4 down, config 4: 507 vs 759 us); int8 gate/up measured 1190 vs
-    // 1213 us (config 5).
-    if constexpr (W4 && GATEUP) {
+    // int4 weights: the scalar-address kernel. Gate/up: config 4 1203 ->
+    // 1060 us, config 5 780 -> 766 us, config 3 209 -> 201 us. Down (without
+    // a VGPR cap; capped at 128 its unrolled loop spills): config 3 106 ->
+    // 99 us, config 4 509 -> 501 us. int8 weights keep mfma_dma_kernel
+    // (config 5 int8 gate/up 1186 vs 1214 us).
+    if constexpr (W4) {
         if (a.w_reuse) launch_mfma_sa_h<W4, EPI, GATEUP, PD, false>(a, g, grid_tiles, st);
         else launch_mfma_sa_h<W4, EPI, GATEUP, PD, true>(a, g, grid_tiles, st);
         return;
