@@ -355,7 +355,7 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemv_kernel(DotArgs a, MatGeom 
         const float u = __shfl(v, (lane & 31) + 32);
         if (lane < 32) {
             const float h = silu_mul(v, u);
-            a.out[(size_t)r * a.out_stride + o] = h;
+            if (!(EPI == EPI_B32 && a.hq)) a.out[(size_t)r * a.out_stride + o] = h;   // else only hq / sh are read
             if (EPI == EPI_B32 && a.hq) {
                 const float m = warp_max(fabsf(h), 32);
                 float sc = __fdiv_rn(m, 127.0f);

@@ -247,7 +247,8 @@ __global__ __launch_bounds__(256) void mfma_kernel(DotArgs a, MatGeom g, const i
             const int row = r0 + acc_row(i, lane);
             const float h = silu_mul(v[0][i], v[1][i]);
             const bool ok = row < rend && o < ((g.O + 31) & ~31);
-            if (ok) a.out[(size_t)row * a.out_stride + o] = h;
+            // with the h quantisation fused, only hq / sh are read downstream
+            if (ok && !(EPI == EPI_B32 && a.hq)) a.out[(size_t)row * a.out_stride + o] = h;
             if (EPI == EPI_B32 && a.hq) {
                 // one h row's 32 channels live in the 32 lanes of this half-wave
                 const float m = warp_max(fabsf(h), 32);
@@ -537,7 +538,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATEUP || !
             const int row = r0 + acc_row(i, lane);
             const float h = silu_mul(v[0][i], v[1][i]);
             const bool ok = row < rend && o < ((g.O + 31) & ~31);
-            if (ok) a.out[(size_t)row * a.out_stride + o] = h;
+            // with the h quantisation fused, only hq / sh are read downstream
+            if (ok && !(EPI == EPI_B32 && a.hq)) a.out[(size_t)row * a.out_stride + o] = h;
             if (EPI == EPI_B32 && a.hq) {
                 const float m = warp_max(fabsf(h), 32);
                 float sc = __fdiv_rn(m, 127.0f);
@@ -828,7 +830,8 @@ __global__ __launch_bounds__(256) void mfma_sa_kernel(DotArgs a, MatGeom g) {
             const int row = r0 + acc_row(i, lane);
             const float h = silu_mul(v[0][i], v[1][i]);
             const bool ok = row < rend && o < ((g.O + 31) & ~31);
-            if (ok) a.out[(size_t)row * a.out_stride + o] = h;
+            // with the h quantisation fused, only hq / sh are read downstream
+            if (ok && !(EPI == EPI_B32 && a.hq)) a.out[(size_t)row * a.out_stride + o] = h;
             if (EPI == EPI_B32 && a.hq) {
                 const float m = warp_max(fabsf(h), 32);
                 float sc = __fdiv_rn(m, 127.0f);
