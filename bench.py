@@ -413,8 +413,25 @@ def main():
     assert hip.init([0]) == 1, "coli_hip_init failed"
     arm = {"auto": -1, "gemv": hip.ARM_GEMV, "mfma": hip.ARM_MFMA}[args.arm]
     ga = args.act_group
+    # The decode (HBM) and prefill (MFMA) halves of the metric first, on the
+    # 160-expert layer (config 4 reuses config 2's resident experts), then
+    # the headline configuration.
+    wl = {}
+    if not args.no_detail:
+        shared = None
+        for cid in (2, 4):
+            if cid == args.config:
+                continue
+            c2 = dict(CONFIGS[cid])
+            c2["seed"] = 2
+            st = DEFAULT_STEPS[cid]
+            s, shared = run_workload(hip, c2, "int4", ga, -1, st, max(2, st // 10), layers=shared,
+                                     pcie=not args.no_pcie)
+            wl[s["workload"]] = s
+        del shared
     head, layers = run_workload(hip, cfg, args.wfmt, ga, arm, steps, warmup, use_graph=not args.no_graph,
                                 pcie=not args.no_pcie)
+    del layers
     line = {
         "metric": METRIC,
         "value": head["value"],
@@ -438,23 +455,8 @@ def main():
         "detail": {k: v for k, v in head.items() if k not in ("value", "unit", "steps", "warmup", "ms_per_step",
                                                              "roofline", "workload")},
     }
-    if not args.no_detail:
-        # the decode (HBM) and prefill (MFMA) halves of the metric, on the
-        # 160-expert layer; config 4 reuses config 2's resident experts
-        del layers
-        wl = {}
-        shared = None
-        for cid in (2, 4):
-            if cid == args.config:
-                continue
-            c2 = dict(CONFIGS[cid])
-            c2["seed"] = 2
-            st = DEFAULT_STEPS[cid]
-            s, shared = run_workload(hip, c2, "int4", ga, -1, st, max(2, st // 10), layers=shared,
-                                     pcie=not args.no_pcie)
-            wl[s["workload"]] = s
+    if wl:
         line["detail"]["workloads"] = wl
-        del shared
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg, args.wfmt, ga, args.cpu_seconds)
     else:
