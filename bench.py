@@ -459,6 +459,9 @@ def main():
         line["detail"]["workloads"] = wl
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg, args.wfmt, ga, args.cpu_seconds)
+        if args.config != 2 and not args.no_detail:   # BASELINE's plan: also the decode layer (config 2)
+            c2 = dict(CONFIGS[2])
+            line["detail"]["cpu_baseline_cfg2"] = cpu_baseline(c2, "int4", ga, args.cpu_seconds / 2)
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)

@@ -815,3 +815,38 @@ def test_large_layer_cfg5_sampled(hip, orc, fmt):
     ref = orc.moe_forward(x, ids, w, ora, 32, subset=sub, nthreads=8)
     assert np.array_equal(o1[sub], ref[sub]), nerr(o1[sub], ref[sub])
     assert np.all(np.isfinite(o1))
+
+
+def _aliased_case(hip, orc, fmt, seed, E, D, I, S, n_dist, zipf):
+    """E expert slots aliasing n_dist distinct uploaded experts, so a dispatch
+    has the configuration's routing, expert-offset table and M-tile count."""
+    rng = np.random.default_rng(seed)
+    gpu, ora = _experts(rng, n_dist, D, I, fmt, 32, orc, hip)
+    eset = hip.ExpertSet([gpu[e % n_dist] for e in range(E)])
+    ora_full = [ora[e % n_dist] for e in range(E)]
+    x = rng.standard_normal((S, D)).astype(np.float32)
+    logits = synth.zipf_logits(rng, S, E) if zipf else synth.normal_logits(rng, S, E)
+    return gpu, ora_full, eset, x, logits
+
+
+@pytest.mark.parametrize("fmt", [qt.FMT_I4G, qt.FMT_I8G])
+def test_batched_layer_cfg3_all_tokens(hip, orc, fmt):
+    """BASELINE config 3 at its shape: 160 expert slots, 64 tokens, Zipf(1.1)
+    top-8 (1-40 rows per expert), every token bit-identical to the oracle."""
+    say("config 3, 160 slots", fmt)
+    gpu, ora, eset, x, logits = _aliased_case(hip, orc, fmt, 3160 + fmt, 160, 5120, 1536, 64, 24, True)
+    out, ids, w = _run_layer(hip, eset, x, logits, 8, 32, -1)
+    ref = orc.moe_forward(x, ids, w, ora, 32, nthreads=8)
+    assert np.array_equal(out, ref), nerr(out, ref)
+
+
+def test_prefill_layer_cfg4_sampled(hip, orc):
+    """BASELINE config 4 at its shape: 160 expert slots, 2048 tokens, Zipf(1.1)
+    top-8 (16,384 rows, popular experts over many M tiles: weight-reuse
+    dispatch), 64 sampled tokens bit-identical to the oracle."""
+    say("config 4, 160 slots")
+    gpu, ora, eset, x, logits = _aliased_case(hip, orc, qt.FMT_I4G, 4160, 160, 5120, 1536, 2048, 24, True)
+    out, ids, w = _run_layer(hip, eset, x, logits, 8, 32, -1)
+    sub = np.arange(0, 2048, 32)
+    ref = orc.moe_forward(x, ids, w, ora, 32, subset=sub, nthreads=8)
+    assert np.array_equal(out[sub], ref[sub]), nerr(out[sub], ref[sub])
