@@ -578,7 +578,7 @@ def test_golden_layer_bit_exact(hip, arm):
         assert bout.download(np.float32, (S, D)).tobytes() == f[f"y_ga{ga}"].tobytes(), ga
 
 
-@pytest.mark.parametrize("S,k,E", [(600, 8, 40), (300, 16, 24), (1100, 1, 12)])
+@pytest.mark.parametrize("S,k,E", [(600, 8, 40), (300, 16, 24), (1100, 1, 12), (512, 8, 256), (500, 8, 160), (256, 16, 512), (4096, 1, 7)])
 def test_expert_table_many_passes(hip, orc, S, k, E):
     """The device-built expert-offset table for batches that take several
     placement passes (and multi-word token masks) equals the oracle's, and the
