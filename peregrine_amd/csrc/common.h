@@ -96,6 +96,7 @@ struct RowPlan {
     const int *mt_exp;     // [T] M-tile -> descriptor index
     const int *mt_row0;    // [T] first row of the tile
     const int *mt_rend;    // [T] one past the last row of that expert
+    const int *mt_first;   // [T] the first M tile of that expert (its tiles are consecutive)
     const int *counts;     // [2] {R, T} as built on the device (or host)
     const ExpertDesc *row_desc;  // optional [R]: row r's descriptor, written by the router
 };
@@ -289,7 +290,7 @@ struct TableOut {
     int *uexp, *off;   // [E], [E+1]
     int *row_tok, *row_kk, *row_exp;  // [R]
     int *tok_rows, *tok_kk;           // [S*k]: each token's rows in union order (-1 pads), their top-k slot
-    int *mt_exp, *mt_row0, *mt_rend;  // [Tmax]
+    int *mt_exp, *mt_row0, *mt_rend, *mt_first;  // [Tmax]
 };
 void launch_synth_fill(void *dst, size_t n, int kind, float a, float b, uint64_t seed, hipStream_t st);
 // work: table_work_ints(S, k, E) ints of device scratch, fully rewritten by every call

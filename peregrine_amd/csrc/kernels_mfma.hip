@@ -601,7 +601,7 @@ struct SaStage {
     static constexpr int BYTES = S + 8 * 128;
 };
 
-template <bool W4, int EPI, bool GATEUP, int PD, bool WNT>
+template <bool W4, int EPI, bool GATEUP, int PD, bool WNT, bool XO = false>
 __global__ __launch_bounds__(256) void mfma_sa_kernel(DotArgs a, MatGeom g) {
     constexpr int NSUB = 2;
     typedef SaStage<W4> ST;
@@ -612,11 +612,33 @@ __global__ __launch_bounds__(256) void mfma_sa_kernel(DotArgs a, MatGeom g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds_u8[];   // [NSTG][ST::BYTES], then sxl
 
     const int lane = threadIdx.x & 63, wave = wave_id();
-    const int tile = blockIdx.y;
+    // XO (dispatches that re-read each expert's weights over several M
+    // tiles): workgroup L runs on XCD L mod 8, and each XCD takes a
+    // contiguous run of the items in (expert, group of XO_G tiles, slab,
+    // tile) order. The tiles of a group read each weight slab through one L2
+    // back to back, and the group's activation rows (XO_G x 32 rows) stay in
+    // that L2 across the slabs. An expert whose tiles are [ts, ts + nt) owns
+    // items [NS * ts, NS * (ts + nt)).
+    int tile = blockIdx.y, slab = blockIdx.x;
+    if constexpr (XO) {
+        constexpr int XO_G = 8;
+        const int T = a.plan.counts[1], NS = (int)gridDim.x, n = NS * T;
+        const int L = slab + NS * (int)blockIdx.y, chunk = (n + 7) >> 3;
+        const int seq = L >> 3, item = (L & 7) * chunk + seq;
+        if (seq >= chunk || item >= n) return;
+        const int q = item / NS;                 // a tile of the item's expert
+        const int ts = a.plan.mt_first[q];
+        const int nt = (a.plan.mt_rend[q] - a.plan.mt_row0[ts] + MT_ROWS - 1) / MT_ROWS;
+        const int local = item - NS * ts;
+        const int grp = local / (NS * XO_G), within = local - grp * NS * XO_G;
+        const int gsize = min(XO_G, nt - grp * XO_G);
+        slab = within / gsize;
+        tile = ts + grp * XO_G + (within - slab * gsize);
+    }
     if (tile >= a.plan.counts[1]) return;
     const int e = a.plan.mt_exp[tile], r0 = a.plan.mt_row0[tile], rend = a.plan.mt_rend[tile];
     const int j = lane & 31, hh = lane >> 5;
-    const int n0 = GATEUP ? ((int)blockIdx.x * 4 + wave) * 32 : ((int)blockIdx.x * 4 + wave) * 32 * NSUB;
+    const int n0 = GATEUP ? (slab * 4 + wave) * 32 : (slab * 4 + wave) * 32 * NSUB;
     const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_u8);
     float *sxl = (float *)(lds_u8 + (size_t)NSTG * ST::BYTES);   // EPI_B32: [nb][32] activation scales
     auto act_row = [&](int r) { return a.act_identity ? r : a.plan.row_act[r]; };
@@ -633,7 +655,7 @@ __global__ __launch_bounds__(256) void mfma_sa_kernel(DotArgs a, MatGeom g) {
     // to its last tile (never stored)
     const int mat = GATEUP ? (wave >> 1) : 2;
     const int ntile = g.Op / TILE_O;
-    int wt = GATEUP ? (int)blockIdx.x * 4 + 2 * (wave & 1) + hh : (int)blockIdx.x * 8 + 2 * wave + hh;
+    int wt = GATEUP ? slab * 4 + 2 * (wave & 1) + hh : slab * 8 + 2 * wave + hh;
     if (wt >= ntile) wt = ntile - 1;
     const uint8_t *base_w = uniform_ptr(a.desc[e].w[mat]);
     const uint8_t *base_s = uniform_ptr(a.desc[e].sc[mat]);
@@ -645,7 +667,7 @@ __global__ __launch_bounds__(256) void mfma_sa_kernel(DotArgs a, MatGeom g) {
     if constexpr (!W4) {
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
-            int t = GATEUP ? (int)blockIdx.x * 4 + 2 * (wave & 1) + q : (int)blockIdx.x * 8 + 2 * wave + q;
+            int t = GATEUP ? slab * 4 + 2 * (wave & 1) + q : slab * 8 + 2 * wave + q;
             if (t >= ntile) t = ntile - 1;
             tile_w8[q] = __builtin_amdgcn_readfirstlane((uint32_t)t * tile_w);
         }
@@ -861,13 +883,13 @@ static size_t mfma_sa_lds(const MatGeom &g) {
     return (size_t)(PD + 2) * SaStage<W4>::BYTES + (EPI == EPI_B32 ? (size_t)(g.nb + 1) / 2 * 2 * 32 * sizeof(float) : 0);
 }
 
-template <bool W4, int EPI, bool GATEUP, int PD, bool WNT>
+template <bool W4, int EPI, bool GATEUP, int PD, bool WNT, bool XO = false>
 static void launch_mfma_sa_h(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
     const int ch_per_wg = GATEUP ? 4 * 32 : 4 * 32 * 2;
     const int span = GATEUP ? ((g.O + 31) & ~31) : g.O;
     dim3 grid((unsigned)((span + ch_per_wg - 1) / ch_per_wg), (unsigned)grid_tiles);
     const size_t lds = mfma_sa_lds<W4, EPI, PD>(g);
-    auto kern = mfma_sa_kernel<W4, EPI, GATEUP, PD, WNT>;
+    auto kern = mfma_sa_kernel<W4, EPI, GATEUP, PD, WNT, XO>;
     static size_t opted[LDS_OPT_DEVICES];
     lds_opt_in((const void *)kern, lds, opted);
     launch_k(kern, grid, dim3(256), lds, st, a, g);
@@ -922,7 +944,9 @@ static void launch_mfma_dma(const DotArgs &a, const MatGeom &g, int grid_tiles, 
     // 99 us, config 4 509 -> 501 us. int8 weights keep mfma_dma_kernel
     // (config 5 int8 gate/up 1186 vs 1214 us).
     if constexpr (W4) {
-        if (a.w_reuse) launch_mfma_sa_h<W4, EPI, GATEUP, PD, false>(a, g, grid_tiles, st);
+        // weight-reuse dispatches in the XCD-aware expert-major order: config 4
+        // gate/up fetch 3.69 -> 2.60 GB, down 1.50 -> 1.01 GB, step 1.5% faster
+        if (a.w_reuse) launch_mfma_sa_h<W4, EPI, GATEUP, PD, false, true>(a, g, grid_tiles, st);
         else launch_mfma_sa_h<W4, EPI, GATEUP, PD, true>(a, g, grid_tiles, st);
         return;
     }

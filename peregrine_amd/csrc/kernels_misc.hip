@@ -548,6 +548,7 @@ __device__ void table_offsets(int n_u, const int *uex, const int *cnt, int *base
         t.mt_exp[q] = uex[lo];
         t.mt_row0[q] = offs[lo] + MT_ROWS * (q - mts[lo]);
         t.mt_rend[q] = offs[lo + 1];
+        t.mt_first[q] = mts[lo];
     }
     __syncthreads();
 }

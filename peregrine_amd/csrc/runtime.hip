@@ -784,7 +784,7 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
     int T = 0;
     for (int i = 0; i < count; i++) T += (rows[i] + MT_ROWS - 1) / MT_ROWS;
     const int s_n = red ? red->s_n : 0;
-    const size_t n_int = (size_t)total /*row_exp*/ + 3 * (size_t)T + 2 + (red ? (size_t)(s_n + 1) + total : 0);
+    const size_t n_int = (size_t)total /*row_exp*/ + 4 * (size_t)T + 2 + (red ? (size_t)(s_n + 1) + total : 0);
     const size_t desc_b = round_up((size_t)count * sizeof(ExpertDesc), 16);
     const size_t meta_b = desc_b + n_int * 4 + (red ? (size_t)total * 4 : 0);
     const size_t xb = (size_t)total * D * 4;
@@ -810,15 +810,18 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
     }
     int *hi = (int *)(hm + desc_b);
     int *row_exp = hi, *mt_exp = row_exp + total, *mt_row0 = mt_exp + T, *mt_rend = mt_row0 + T;
-    int *counts = mt_rend + T;
+    int *mt_first = mt_rend + T;
+    int *counts = mt_first + T;
     int *rp = counts + 2, *ri = rp + (red ? s_n + 1 : 0);
     float *rwv = (float *)(ri + (red ? total : 0));
     for (int i = 0, r = 0, t = 0; i < count; i++) {
         for (int q = 0; q < rows[i]; q++) row_exp[r + q] = i;
+        const int t0 = t;
         for (int q = 0; q < rows[i]; q += MT_ROWS, t++) {
             mt_exp[t] = i;
             mt_row0[t] = r + q;
             mt_rend[t] = r + rows[i];
+            mt_first[t] = t0;
         }
         r += rows[i];
     }
@@ -839,7 +842,8 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
     plan.mt_exp = di + total;
     plan.mt_row0 = di + total + T;
     plan.mt_rend = di + total + 2 * T;
-    plan.counts = di + total + 3 * T;
+    plan.mt_first = di + total + 3 * T;
+    plan.counts = di + total + 4 * T;
     DispatchOpts opt;
     opt.w_reuse = total >= 2 * MT_ROWS * count;   // about two or more M tiles per expert
     // x ([total][D] f32) is staged in the y buffer, which has exactly that
@@ -1377,7 +1381,7 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
 
     // table layout in one buffer
     const size_t n_int =
-        4 + (size_t)E + (E + 1) + 3 * (size_t)R + 2 * (size_t)R + 3 * (size_t)tmax + table_work_ints(S, k, E);
+        4 + (size_t)E + (E + 1) + 3 * (size_t)R + 2 * (size_t)R + 4 * (size_t)tmax + table_work_ints(S, k, E);
     Scratch s{};
     int *p = nullptr;
     if (fixed_scratch) {
@@ -1423,6 +1427,8 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
     t.mt_row0 = p;
     p += tmax;
     t.mt_rend = p;
+    p += tmax;
+    t.mt_first = p;
     p += tmax;
     int *tbl_work = p;
     c->tbl_view = t;
@@ -1483,6 +1489,7 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
         plan.mt_exp = t.mt_exp;
         plan.mt_row0 = t.mt_row0;
         plan.mt_rend = t.mt_rend;
+        plan.mt_first = t.mt_first;
         plan.counts = t.hdr;
     }
     run_experts(c, prof, set->desc_dev, plan, gg, gd, x_dev, S, false, R, tmax, ga, arm, s, opt);
