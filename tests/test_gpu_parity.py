@@ -850,3 +850,36 @@ def test_prefill_layer_cfg4_sampled(hip, orc):
     sub = np.arange(0, 2048, 32)
     ref = orc.moe_forward(x, ids, w, ora, 32, subset=sub, nthreads=8)
     assert np.array_equal(out[sub], ref[sub]), nerr(out[sub], ref[sub])
+
+
+def test_device_exp_equals_glibc_through_the_routers(hip, orc):
+    """The kernels' exp (expf_glibc) against glibc's expf, through the two
+    routers. Softmax: the top logit is 0 and the other 15 kept logits are the
+    arguments d in [-104, 0], so the weights are exp(d) / sum, subnormal
+    exp(d) included (d below -87.3). Sigmoid (no renormalisation): the
+    weights are 1 / (1 + exp(-l)) for l in [-89, 104], exp's overflow
+    included. Bit-identical to the oracle, which calls glibc's expf."""
+    say("device exp sweep")
+    rng = np.random.default_rng(2718)
+    S, E, k = 8192, 16, 16
+    d = np.linspace(-104.0, 0.0, S * (E - 1), dtype=np.float32)
+    d = rng.permutation(d).reshape(S, E - 1)
+    logits = np.concatenate([np.zeros((S, 1), np.float32), d], axis=1)
+    bl = hip.DeviceBuffer.from_array(logits)
+    bids, bw = hip.DeviceBuffer(S * k * 4), hip.DeviceBuffer(S * k * 4)
+    hip.route_softmax_topk_dev(0, bl.ptr, S, E, k, bids.ptr, bw.ptr)
+    hip.pipe_sync(0)
+    ids, w = orc.route_softmax_topk(logits, k)
+    assert np.array_equal(bids.download(np.int32, (S, k)), ids)
+    assert bw.download(np.float32, (S, k)).tobytes() == w.tobytes()
+    assert np.any((w > 0) & (w < np.finfo(np.float32).tiny))   # the subnormal range was reached
+
+    lg = rng.permutation(np.linspace(-89.0, 104.0, S * E, dtype=np.float32)).reshape(S, E)
+    bl2 = hip.DeviceBuffer.from_array(lg)
+    zero = hip.DeviceBuffer.from_array(np.zeros(E, np.float32))
+    bk = hip.DeviceBuffer(S * 4)
+    hip.route_sigmoid_topk_dev(0, bl2.ptr, zero.ptr, S, E, k, bids.ptr, bw.ptr, bk.ptr, False, 1.0, 0.0)
+    hip.pipe_sync(0)
+    ids2, w2, _ = orc.route_sigmoid(lg, np.zeros(E, np.float32), k, False, 1.0, 0.0)
+    assert np.array_equal(bids.download(np.int32, (S, k)), ids2)
+    assert bw.download(np.float32, (S, k)).tobytes() == w2.tobytes()
