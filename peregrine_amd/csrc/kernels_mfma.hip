@@ -313,12 +313,10 @@ struct DmaStage {
     static constexpr int BYTES = WAVE0 + 4 * WAVE_BYTES;
 };
 
-// The int4 down projection is capped at 128 VGPRs so that four waves share a
-// SIMD (its stages and activation scales fit four workgroups per CU up to
-// K = 2048). Measured: config 4 down 527 -> 497 us; configs 3 and 5 flat. The
-// gate/up kernels (138 VGPRs, LDS for three workgroups per CU) and the int8
-// down projection are left uncapped (capped, it spills eight registers:
-// config 5 int8 down 735 vs 630 us).
+// Dispatches with int8 weights run this kernel (int4 ones run
+// mfma_sa_kernel below). An int4 instantiation caps the down projection at
+// 128 VGPRs (four waves per SIMD); int8 ones are left uncapped (capped, the
+// int8 down projection spills eight registers: config 5 735 vs 630 us).
 template <bool W4, int EPI, bool GATEUP, int NSUB, int PD, bool WNT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATEUP || !W4 ? 1 : 4))) void mfma_dma_kernel(DotArgs a, MatGeom g) {
     static_assert(NSUB == 2, "a wave's weight copy covers two 32-column subtiles");
@@ -948,10 +946,10 @@ static void launch_mfma_dma(const DotArgs &a, const MatGeom &g, int grid_tiles, 
         // gate/up fetch 3.69 -> 2.60 GB, down 1.50 -> 1.01 GB, step 1.5% faster
         if (a.w_reuse) launch_mfma_sa_h<W4, EPI, GATEUP, PD, false, true>(a, g, grid_tiles, st);
         else launch_mfma_sa_h<W4, EPI, GATEUP, PD, true>(a, g, grid_tiles, st);
-        return;
+    } else {
+        if (a.w_reuse) launch_mfma_dma_h<W4, EPI, GATEUP, PD, false>(a, g, grid_tiles, st);
+        else launch_mfma_dma_h<W4, EPI, GATEUP, PD, true>(a, g, grid_tiles, st);
     }
-    if (a.w_reuse) launch_mfma_dma_h<W4, EPI, GATEUP, PD, false>(a, g, grid_tiles, st);
-    else launch_mfma_dma_h<W4, EPI, GATEUP, PD, true>(a, g, grid_tiles, st);
 }
 
 // COLI_HIP_MFMA_DMA: -1 (default) the LDS-staged kernel wherever its stages
