@@ -362,6 +362,36 @@ void free_ctx(Ctx *c) {
 }
 
 
+// Every context of this process, released (device selected for each).
+void release_all() {
+    for (int i = 0; i < g_nctx; i++)
+        if (select_ctx(&g_ctx[i])) free_ctx(&g_ctx[i]);
+    g_nctx = 0;
+    g_cur_dev = -1;
+}
+
+// Builds one device context: its stream, the host-visible GEMV wait flag and
+// the address of its copy of the fixed scratch array; reports the device.
+int open_ctx(Ctx *c) {
+    g_cur_dev = -1;
+    if (!select_ctx(c)) return 0;
+    hipDeviceProp_t prop{};
+    if (!hip_ok(hipGetDeviceProperties(&prop, c->device), "init: device properties") ||
+        !hip_ok(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "init: stream") ||
+        !hip_ok(hipHostMalloc((void **)&c->wait_flag, sizeof(int), hipHostMallocMapped | hipHostMallocCoherent),
+                "init: wait flag") ||
+        !hip_ok(hipHostGetDevicePointer((void **)&c->wait_flag_dev, c->wait_flag, 0), "init: wait flag mapping") ||
+        !hip_ok(hipGetSymbolAddress((void **)&c->fixed_scratch, HIP_SYMBOL(scratch)), "init: fixed scratch"))
+        return 0;
+    *c->wait_flag = 0;
+    int lds = 0;
+    if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, c->device) != hipSuccess) lds = 0;
+    set_lds_limit(lds);
+    std::fprintf(stderr, "[HIP] device %d: %s (%s), %.1f GB HBM, %d CUs, %d KB LDS per workgroup\n", c->device,
+                 prop.name, prop.gcnArchName, prop.totalGlobalMem / 1e9, prop.multiProcessorCount, lds / 1024);
+    return 1;
+}
+
 int make_geom(int fmt, int I, int O, int gs, MatGeom *g) {
     const bool grouped = fmt == COLI_HIP_FMT_I4G || fmt == COLI_HIP_FMT_I8G;
     if (I < 1 || O < 1) return fail("tensor shape must be positive");
@@ -955,71 +985,42 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
 // ============================================================================
 extern "C" {
 
+// The ordinal list is checked as a whole before anything is built: every
+// entry must name a visible device and none may repeat (0 otherwise, and the
+// contexts of an earlier init stay as they were). Then the earlier contexts
+// are released and one is built per ordinal, in list order; if building one
+// fails, every context built so far is released again.
 int coli_hip_init(const int *devices, int count) {
-    int available = 0;
     if (!devices || count < 1 || count > COLI_HIP_MAX_DEVICES) return 0;
-    if (!hip_ok(hipGetDeviceCount(&available), "device discovery")) return 0;
-    for (int i = 0; i < g_nctx; i++) free_ctx(&g_ctx[i]);
-    g_nctx = 0;
-    g_cur_dev = -1;
+    int visible = 0;
+    if (!hip_ok(hipGetDeviceCount(&visible), "init: counting HIP devices")) return 0;
     for (int i = 0; i < count; i++) {
-        const int device = devices[i];
-        if (device < 0 || device >= available) {
-            std::fprintf(stderr, "[HIP] invalid device %d (available: 0..%d)\n", device, available - 1);
-            for (int j = 0; j < g_nctx; j++) free_ctx(&g_ctx[j]);
-            g_nctx = 0;
+        if (devices[i] < 0 || devices[i] >= visible) {
+            std::fprintf(stderr, "[HIP] init: ordinal %d names no device (%d visible)\n", devices[i], visible);
             return 0;
         }
-        if (find_ctx(device)) {
-            std::fprintf(stderr, "[HIP] duplicate device %d\n", device);
-            for (int j = 0; j < g_nctx; j++) free_ctx(&g_ctx[j]);
-            g_nctx = 0;
-            return 0;
-        }
-        Ctx *c = &g_ctx[g_nctx];
+        for (int j = 0; j < i; j++)
+            if (devices[j] == devices[i]) {
+                std::fprintf(stderr, "[HIP] init: ordinal %d appears twice in the list\n", devices[i]);
+                return 0;
+            }
+    }
+    release_all();
+    for (int i = 0; i < count; i++) {
+        Ctx *c = &g_ctx[i];
         *c = Ctx{};
-        c->device = device;
-        if (!select_ctx(c)) return 0;
-        hipDeviceProp_t prop{};
-        if (!hip_ok(hipGetDeviceProperties(&prop, device), "device properties") ||
-            !hip_ok(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "stream creation")) {
-            for (int j = 0; j < g_nctx; j++) free_ctx(&g_ctx[j]);
-            g_nctx = 0;
-            return 0;
-        }
-        if (!hip_ok(hipHostMalloc((void **)&c->wait_flag, sizeof(int), hipHostMallocMapped | hipHostMallocCoherent),
-                    "wait flag allocation") ||
-            !hip_ok(hipHostGetDevicePointer((void **)&c->wait_flag_dev, c->wait_flag, 0), "wait flag mapping")) {
+        c->device = devices[i];
+        if (!open_ctx(c)) {
             free_ctx(c);
-            for (int j = 0; j < g_nctx; j++) free_ctx(&g_ctx[j]);
-            g_nctx = 0;
+            release_all();
             return 0;
         }
-        *c->wait_flag = 0;
-        if (!hip_ok(hipGetSymbolAddress((void **)&c->fixed_scratch, HIP_SYMBOL(scratch)), "fixed scratch mapping")) {
-            free_ctx(c);
-            for (int j = 0; j < g_nctx; j++) free_ctx(&g_ctx[j]);
-            g_nctx = 0;
-            return 0;
-        }
-        g_nctx++;
-        int lds = 0;
-        if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device) != hipSuccess) lds = 0;
-        set_lds_limit(lds);
-        std::fprintf(stderr, "[HIP] device %d: %s (%s), %.1f GB HBM, %d CUs, %d KB LDS per workgroup\n", device,
-                     prop.name, prop.gcnArchName, prop.totalGlobalMem / 1e9, prop.multiProcessorCount, lds / 1024);
+        g_nctx = i + 1;
     }
     return 1;
 }
 
-void coli_hip_shutdown(void) {
-    for (int i = 0; i < g_nctx; i++) {
-        if (!select_ctx(&g_ctx[i])) continue;
-        free_ctx(&g_ctx[i]);
-    }
-    g_nctx = 0;
-    g_cur_dev = -1;
-}
+void coli_hip_shutdown(void) { release_all(); }
 
 int coli_hip_device_count(void) { return g_nctx; }
 

@@ -54,6 +54,18 @@ def test_probe_init_meminfo(hip):
     assert total > 100e9 and 0 < free <= total
 
 
+def test_init_rejects_bad_ordinal_lists(hip):
+    """A list naming a missing device or one device twice is refused as a
+    whole and leaves the contexts of the earlier init in place."""
+    say("init validation")
+    assert hip.init([0, 0]) == 0
+    assert hip.init([hip.probe_device_count()]) == 0
+    assert hip.init([-1]) == 0
+    assert hip.device_count() == 1
+    free, total = hip.mem_info(0)
+    assert 0 < free <= total
+
+
 FORMATS = [(qt.FMT_I4G, 32), (qt.FMT_I4G, 128), (qt.FMT_I4, 0), (qt.FMT_I8G, 32), (qt.FMT_I8, 0)]
 
 
