@@ -258,7 +258,17 @@ struct DotArgs {   // shared by the GEMV and MFMA arms
     int *wait_failed;                                                   // GEMV: host-visible word, set to 1 when one does
     int w_reuse;                                                        // MFMA arm: M tiles re-read each expert's weights
     RouteArgs route;                                                    // gate/up GEMV: logits != null -> fused router
+    // down GEMV, one token (rows 0..n-1 in top-k order): the last workgroup
+    // to finish an output tile also writes tail_out over that tile, the
+    // router-weighted sum of the rows in row order (the combine's order);
+    // tail_ctr holds one arrival counter per tile, zero between dispatches
+    float *tail_out;
+    const float *tail_w;
+    int *tail_ctr;
 };
+// output tiles the tail counters cover (down GEMV tiles are 64 channels)
+constexpr int GEMV_TAIL_TILES = 4096;
+constexpr int GEMV_TAIL_MAXK = 16;
 // grid_rows / grid_tiles: host-side upper bounds; the kernels read the true
 // counts from plan.counts and idle the excess workgroups.
 void launch_gemv_gateup(const DotArgs &a, const MatGeom &g, int act, int grid_rows, hipStream_t st);

@@ -80,6 +80,42 @@ __device__ __forceinline__ void spin_until_geq(int *ctr, int target, int limit, 
     if ((threadIdx.x & 63) == 0) __hip_atomic_store(failed, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+// The chain wave of a down-GEMV workgroup, after its y stores: counts the
+// workgroup in for its output tile; the workgroup that completes the tile's
+// count (every row done) sums the tile's rows, out[o] = (((0 + w0*y0) +
+// w1*y1) + ...) in row order, rounded multiply then rounded add, as
+// combine_tok_kernel does for one token, and resets the counter for the next
+// dispatch.
+// Visibility across the XCDs' L2s without a whole-cache write-back and
+// invalidate (an agent-scope fence per workgroup costs ~18 us at config 2):
+// the y stores and the last workgroup's y loads are agent-scope atomics
+// (write-through / coherent reads of just those lines), the stores have
+// completed (vmcnt 0) before the count is incremented, the count is an
+// agent-scope read-modify-write, and the loads issue only after it returns.
+__device__ __forceinline__ void tail_combine(const DotArgs &a, int O, int nrows, int o) {
+    const int lane = threadIdx.x & 63;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    int old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(&a.tail_ctr[blockIdx.x], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __shfl(old, 0);
+    if (old != nrows - 1) return;   // uniform
+    asm volatile("" ::: "memory");
+    const int oc = o < O ? o : O - 1;
+    float yv[GEMV_TAIL_MAXK], wv[GEMV_TAIL_MAXK];
+#pragma unroll
+    for (int j = 0; j < GEMV_TAIL_MAXK; ++j) {   // every load issued before the sum
+        const int jj = j < nrows ? j : 0;
+        yv[j] = __hip_atomic_load(&a.out[(size_t)jj * a.out_stride + oc], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        wv[j] = a.tail_w[jj];
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < GEMV_TAIL_MAXK; ++j)
+        if (j < nrows) acc = __fadd_rn(acc, __fmul_rn(wv[j], yv[j]));
+    if (o < O) a.tail_out[o] = acc;
+    if (lane == 0) __hip_atomic_store(&a.tail_ctr[blockIdx.x], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // NW streaming waves plus one chain wave. K is walked in rounds of NW*CH
 // blocks; in round c streaming wave w owns blocks c*NW*CH + w*CH + [0, CH).
 // A streaming wave issues its CH weight (and scale) loads for a round as one
@@ -366,7 +402,12 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemv_kernel(DotArgs a, MatGeom 
             }
         }
     } else {
-        if (o < g.O) a.out[(size_t)r * a.out_stride + o] = v;
+        if (!a.tail_out) {
+            if (o < g.O) a.out[(size_t)r * a.out_stride + o] = v;
+        } else {
+            if (o < g.O) __hip_atomic_store(&a.out[(size_t)r * a.out_stride + o], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            tail_combine(a, g.O, nrows, o);
+        }
     }
 }
 

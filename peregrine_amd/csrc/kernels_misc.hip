@@ -225,7 +225,7 @@ void launch_combine_tok(float *out, const float *y, const int *tok_rows, const i
 // ---------------------------------------------------------------------------
 // The reference's own router (peregrine-model/src/router.rs:52-170, after
 // the router matmul), one wavefront per token: sigmoid scores (exp evaluated
-// as exp_cr), greedy top-k over score + bias with the same argmax rounds,
+// as glibc expf), greedy top-k over score + bias with the same argmax rounds,
 // weight = the winner's sigmoid; unfilled slots (0, 0); the negligible tail
 // (router.rs:191-209) dropped when min_share > 0; optional renormalisation
 // over all k slots (+1e-20, summed in slot order); times routed_scale.

@@ -23,6 +23,11 @@ using namespace phip;
 // Host code uses only the per-device address kept in Ctx::fixed_scratch,
 // never this name.
 static __device__ __align__(256) uint8_t scratch[COLI_HIP_FIXED_SCRATCH_BYTES];
+// Per-tile arrival counters of the down GEMV's tail combine: zero at load,
+// and each dispatch leaves them zero again (the tile's last workgroup resets
+// its counter), so no clearing launch is needed. One stream per device uses
+// them; host code uses the address kept in Ctx::tail_ctr.
+static __device__ int tail_ctr[GEMV_TAIL_TILES];
 
 namespace {
 struct Slab;
@@ -88,6 +93,7 @@ struct Ctx {
     // device address of this device's copy of the fixed scratch array (the
     // no-allocation entry point), looked up at init with the device current
     uint8_t *fixed_scratch = nullptr;
+    int *tail_ctr = nullptr;   // this device's copy of tail_ctr[]
     // last device-resident table (for coli_hip_last_table)
     TableOut tbl_view{};
     int tbl_E = 0, tbl_R = 0;
@@ -241,6 +247,13 @@ bool fused_combine_on(int k) {
     return m == 1 || (m == -1 && k <= 2);
 }
 
+// COLI_HIP_TAIL_COMBINE=0 keeps the separate combine launch after a
+// one-token down GEMV (A/B measurement); default on.
+bool tail_combine_on() {
+    static const bool on = !(getenv("COLI_HIP_TAIL_COMBINE") && getenv("COLI_HIP_TAIL_COMBINE")[0] == '0');
+    return on;
+}
+
 int forced_arm() {
     if (g_arm == -2) {
         const char *v = std::getenv("COLI_HIP_ARM");
@@ -381,7 +394,8 @@ int open_ctx(Ctx *c) {
         !hip_ok(hipHostMalloc((void **)&c->wait_flag, sizeof(int), hipHostMallocMapped | hipHostMallocCoherent),
                 "init: wait flag") ||
         !hip_ok(hipHostGetDevicePointer((void **)&c->wait_flag_dev, c->wait_flag, 0), "init: wait flag mapping") ||
-        !hip_ok(hipGetSymbolAddress((void **)&c->fixed_scratch, HIP_SYMBOL(scratch)), "init: fixed scratch"))
+        !hip_ok(hipGetSymbolAddress((void **)&c->fixed_scratch, HIP_SYMBOL(scratch)), "init: fixed scratch") ||
+        !hip_ok(hipGetSymbolAddress((void **)&c->tail_ctr, HIP_SYMBOL(tail_ctr)), "init: tail counters"))
         return 0;
     *c->wait_flag = 0;
     int lds = 0;
@@ -628,6 +642,9 @@ struct DispatchOpts {
     int w_reuse = 0;                    // about two or more M tiles per expert: weights stay cacheable
     const float *combine_w = nullptr;   // one token: down + combine in one launch, weights [k]
     float *combine_out = nullptr;       //   and the layer output [D]
+    const float *tail_w = nullptr;      // one token: the down GEMV's last workgroup per tile combines
+    float *tail_out = nullptr;
+    int *tail_ctr = nullptr;
 };
 
 // The kernel sequence of one dispatch after the activations are on the
@@ -688,6 +705,9 @@ void run_experts(Ctx *c, Prof &prof, const ExpertDesc *desc, const RowPlan &plan
     dd.act_identity = 1;
     dd.act_zero = 0;
     dd.route = RouteArgs{};
+    dd.tail_out = opt.tail_out;
+    dd.tail_w = opt.tail_w;
+    dd.tail_ctr = opt.tail_ctr;
     prof.mark(COLI_HIP_K_DOWN);
     if (arm == COLI_HIP_ARM_GEMV && opt.combine_out) {
         launch_gemv_down_combine(dd, gd, act, opt.n_rows_fixed, opt.combine_w, opt.combine_out, c->stream);
@@ -1473,6 +1493,14 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
         opt.combine_w = w_dev;
         opt.combine_out = out_dev;
     }
+    // otherwise, one token: the down GEMV's tail does the combine
+    const bool tail_c = one_token && !fuse_dc && tail_combine_on() && !g_dbg_dn && k <= GEMV_TAIL_MAXK &&
+                        (gd.O + 63) / 64 <= GEMV_TAIL_TILES;
+    if (tail_c) {
+        opt.tail_w = w_dev;
+        opt.tail_out = out_dev;
+        opt.tail_ctr = c->tail_ctr;
+    }
     RowPlan plan{};
     if (one_token) {
         c->tbl_view.hdr = nullptr;
@@ -1495,7 +1523,7 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
     }
     run_experts(c, prof, set->desc_dev, plan, gg, gd, x_dev, S, false, R, tmax, ga, arm, s, opt);
     prof.mark(COLI_HIP_K_COMBINE);
-    if (fuse_dc) {
+    if (fuse_dc || tail_c) {
         // combined by the down GEMV
     } else if (one_token) {   // rows 0..k-1 of token 0, in top-k order
         launch_combine_tok(out_dev, s.y, nullptr, nullptr, w_dev, 1, k, gd.O, s.ys, c->stream);
