@@ -288,6 +288,12 @@ int select_ctx(Ctx *c) {
 int check_waits(Ctx *c) {
     if (!c->wait_flag || !*(volatile int *)c->wait_flag) return 1;
     *(volatile int *)c->wait_flag = 0;
+    // clear the tail combine's tile counters too (the stream is idle here),
+    // so a faulty dispatch cannot leave later ones a stale count
+    if (c->tail_ctr) {
+        hipMemsetAsync(c->tail_ctr, 0, GEMV_TAIL_TILES * sizeof(int), c->stream);
+        hipStreamSynchronize(c->stream);
+    }
     return fail("GEMV: a bounded wait between the streaming and chain waves gave up; the output of the "
                 "dispatches since the last check is not valid");
 }
