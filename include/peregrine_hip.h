@@ -44,6 +44,9 @@ typedef struct ColiHipGraph ColiHipGraph;
 typedef struct ColiHipExpertSet ColiHipExpertSet;
 
 /* ---- devices: replaces backend_cuda.h:30-40 ---- */
+/* One context (non-blocking stream) per listed ordinal, 1 <= count <= 16.
+ * Returns 0 when an ordinal names no visible device or repeats; the contexts
+ * of an earlier init are then left as they were. Otherwise they are replaced. */
 int coli_hip_init(const int *devices, int count);                  /* coli_cuda_init */
 void coli_hip_shutdown(void);                                      /* coli_cuda_shutdown */
 int coli_hip_device_count(void);                                   /* coli_cuda_device_count */
