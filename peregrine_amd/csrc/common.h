@@ -228,6 +228,9 @@ inline void launch_k(K kern, dim3 grid, dim3 block, size_t lds, hipStream_t st, 
 struct QuantArgs {
     const float *x; int x_stride; int rows; int K; int Kp;
     int8_t *q; int q_stride; float *s; int s_stride; int mode;
+    // optional: the workgroups also copy n16 16-byte words src -> dst (a
+    // host-buffer call's metadata, staged from mapped host memory)
+    const uint4 *copy_src; uint4 *copy_dst; int copy_n16;
 };
 void launch_quant_rows(const QuantArgs &a, hipStream_t st);
 

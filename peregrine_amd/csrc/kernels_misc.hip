@@ -15,7 +15,16 @@ namespace phip {
 // row. Output bytes go to the permuted device layout (perm8) and the row is
 // zero-padded to Kp, so padded weight columns contribute nothing.
 // ---------------------------------------------------------------------------
+// a.copy_n16 words from a.copy_src to a.copy_dst, spread over the grid
+__device__ __forceinline__ void quant_side_copy(const QuantArgs &a) {
+    if (a.copy_n16 <= 0) return;
+    const int nwg = (int)(gridDim.x * gridDim.y), wg = (int)(blockIdx.y * gridDim.x + blockIdx.x);
+    for (int i = wg * (int)blockDim.x + (int)threadIdx.x; i < a.copy_n16; i += nwg * (int)blockDim.x)
+        a.copy_dst[i] = a.copy_src[i];
+}
+
 __global__ __launch_bounds__(1024) void quant_rows_kernel(QuantArgs a) {
+    quant_side_copy(a);
     // ACT_ROW: one workgroup per row; every thread loads its elements in one
     // round, then a block reduction gives the row's amax.
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -53,6 +62,7 @@ __global__ __launch_bounds__(1024) void quant_rows_kernel(QuantArgs a) {
 }
 
 __global__ __launch_bounds__(256) void quant_blocks_kernel(QuantArgs a) {
+    quant_side_copy(a);
     // ACT_B32: 8 elements per thread, a workgroup covers 64 blocks of one row
     const int row = blockIdx.y, nbk = a.Kp / BLK;
     const int b_lo = blockIdx.x * 64, b_hi = min(nbk, b_lo + 64);

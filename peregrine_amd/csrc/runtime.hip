@@ -61,6 +61,7 @@ namespace {
 struct Buf {
     void *p = nullptr;
     size_t cap = 0;
+    void *d = nullptr;   // pinned buffers: the device's address of the mapped host memory
 };
 
 constexpr int GRAPH_CACHE = 16;   // cached expert-group graphs per device
@@ -327,7 +328,14 @@ int reserve_pinned(Ctx *c, Buf &b, size_t bytes) {
     b.p = nullptr;
     b.cap = 0;
     c->gen++;
-    if (!hip_ok(hipHostMalloc(&b.p, bytes, hipHostMallocDefault), "pinned staging allocation")) return 0;
+    // mapped and coherent: kernels read and write it across PCIe directly
+    if (!hip_ok(hipHostMalloc(&b.p, bytes, hipHostMallocMapped | hipHostMallocCoherent), "pinned staging allocation"))
+        return 0;
+    if (!hip_ok(hipHostGetDevicePointer(&b.d, b.p, 0), "pinned staging mapping")) {
+        hipHostFree(b.p);
+        b = Buf{};
+        return 0;
+    }
     b.cap = bytes;
     return 1;
 }
@@ -650,7 +658,11 @@ struct DispatchOpts {
     float *combine_out = nullptr;       //   and the layer output [D]
     const float *tail_w = nullptr;      // one token: the down GEMV's last workgroup per tile combines
     float *tail_out = nullptr;
-    int *tail_ctr = nullptr;
+    int *tail_ctr = nullptr;    // host-buffer calls: the activation quantisation also stages this metadata
+    const void *meta_src = nullptr;
+    void *meta_dst = nullptr;
+    int meta_n16 = 0;
+    hipEvent_t after_quant = nullptr;   // recorded after the activation quantisation (profiling)
 };
 
 // The kernel sequence of one dispatch after the activations are on the
@@ -660,9 +672,11 @@ void run_experts(Ctx *c, Prof &prof, const ExpertDesc *desc, const RowPlan &plan
                  int ga, int arm, const Scratch &s, const DispatchOpts &opt = DispatchOpts()) {
     const int act = epi_act(ga);
     if (!opt.x_quantized) {
-        QuantArgs qa{x_dev, gg.K, rows_x, gg.K, gg.Kp, s.xq, s.xs, s.sx, s.sxs, act};
+        QuantArgs qa{x_dev, gg.K, rows_x, gg.K, gg.Kp, s.xq, s.xs, s.sx, s.sxs, act,
+                     (const uint4 *)opt.meta_src, (uint4 *)opt.meta_dst, opt.meta_n16};
         prof.mark(COLI_HIP_K_QUANT_X);
         launch_quant_rows(qa, c->stream);
+        if (opt.after_quant) hipEventRecord(opt.after_quant, c->stream);
     }
 
     DotArgs da{};
@@ -842,7 +856,8 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
     const int s_n = red ? red->s_n : 0;
     const size_t n_int = (size_t)total /*row_exp*/ + 4 * (size_t)T + 2 + (red ? (size_t)(s_n + 1) + total : 0);
     const size_t desc_b = round_up((size_t)count * sizeof(ExpertDesc), 16);
-    const size_t meta_b = desc_b + n_int * 4 + (red ? (size_t)total * 4 : 0);
+    // (a whole number of 16-byte words: the quantisation kernel stages it)
+    const size_t meta_b = round_up(desc_b + n_int * 4 + (red ? (size_t)total * 4 : 0), 16);
     const size_t xb = (size_t)total * D * 4;
     const size_t ob = red ? (size_t)s_n * D * 4 : xb;
     // every reservation happens here, before any capture (scratch must not
@@ -850,7 +865,7 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
     Scratch s{};
     if (!reserve_rows(c, gg, gd, total, total, ga, &s) || !reserve(c, c->meta, meta_b) ||
         !reserve_pinned(c, c->pin_meta, meta_b) || !reserve_pinned(c, c->pin_x, xb) ||
-        !reserve_pinned(c, c->pin_y, ob) || (red && !reserve(c, c->red_out, ob)))
+        !reserve_pinned(c, c->pin_y, ob))
         return 0;
 
     // stage the call's contents: descriptors, row plan, reduce layout, x
@@ -900,39 +915,44 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
     plan.mt_rend = di + total + 2 * T;
     plan.mt_first = di + total + 3 * T;
     plan.counts = di + total + 4 * T;
+    // No copy engine in the call: the staging buffers are mapped host
+    // memory. The activation quantisation reads x across PCIe and also stages
+    // the metadata into device memory (every later kernel reads it there); the
+    // last kernel (the combine, else the down projection) writes the result
+    // across PCIe. Config 2's call (8 rows, one token out): 89 -> 62.5 us
+    // eager, 79 -> 68.7 us from a cached graph (profiled, the copies alone had
+    // taken 22 us in and 48 us out).
     DispatchOpts opt;
     opt.w_reuse = total >= 2 * MT_ROWS * count;   // about two or more M tiles per expert
-    // x ([total][D] f32) is staged in the y buffer, which has exactly that
-    // shape: the x quantisation reads it before the down projection writes y.
-    float *x_dev = (float *)c->y.p;
-    float *res = red ? (float *)c->red_out.p : s.y;
+    opt.meta_src = c->pin_meta.d;
+    opt.meta_dst = dm;
+    opt.meta_n16 = (int)(meta_b / 16);
+    const float *x_dev = (const float *)c->pin_x.d;
+    Scratch so = s;
+    if (!red) so.y = (float *)c->pin_y.d;   // [total][D], the y buffer's own layout
 
-    // The whole call as stream work: contents in, kernels, result out. The
-    // same sequence runs eagerly or is captured once per shape.
+    // The whole call as stream work. The same sequence runs eagerly or is
+    // captured once per shape. Under profiling, h2d = the quantisation kernel
+    // that reads x across PCIe, d2h = the combine that writes the output
+    // across PCIe (0 without a reduce: the down projection writes it, and its
+    // time is kernel time).
     const bool profile = profiling() != 0;
     auto enqueue = [&](Prof &prof, bool phases) -> int {
         if (phases) hipEventRecord(c->phase_ev[0], c->stream);
-        if (!hip_ok(hipMemcpyAsync(dm, hm, meta_b, hipMemcpyHostToDevice, c->stream), "expert group metadata") ||
-            !hip_ok(hipMemcpyAsync(x_dev, c->pin_x.p, xb, hipMemcpyHostToDevice, c->stream),
-                    "expert group input upload"))
-            return 0;
-        if (phases) hipEventRecord(c->phase_ev[1], c->stream);
+        opt.after_quant = phases ? c->phase_ev[1] : nullptr;
         prof.mark(-1);
-        run_experts(c, prof, (const ExpertDesc *)dm, plan, gg, gd, x_dev, total, true, total, T, ga, arm, s, opt);
+        run_experts(c, prof, (const ExpertDesc *)dm, plan, gg, gd, x_dev, total, true, total, T, ga, arm, so, opt);
+        prof.mark(-1);
+        if (phases) hipEventRecord(c->phase_ev[2], c->stream);
         if (red) {
             const int *drp = plan.counts + 2, *dri = drp + s_n + 1;
             const float *drw = (const float *)(dri + total);
             prof.mark(COLI_HIP_K_COMBINE);
-            launch_combine((float *)c->red_out.p, s.y, drp, dri, drw, s_n, D, s.ys, c->stream);
+            launch_combine((float *)c->pin_y.d, s.y, drp, dri, drw, s_n, D, s.ys, c->stream);
+            prof.mark(-1);
         }
-        prof.mark(-1);
-        if (phases) hipEventRecord(c->phase_ev[2], c->stream);
-        if (!hip_ok(hipGetLastError(), "expert group launch") ||
-            !hip_ok(hipMemcpyAsync(c->pin_y.p, res, ob, hipMemcpyDeviceToHost, c->stream),
-                    "expert group output download"))
-            return 0;
         if (phases) hipEventRecord(c->phase_ev[3], c->stream);
-        return 1;
+        return hip_ok(hipGetLastError(), "expert group launch");
     };
     auto finish = [&]() -> int {
         if (!check_waits(c)) return 0;
