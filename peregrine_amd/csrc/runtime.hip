@@ -81,7 +81,7 @@ struct Ctx {
     hipStream_t stream = nullptr;
     size_t tensor_count = 0, tensor_bytes = 0;
     unsigned gen = 0;   // bumped on every scratch reallocation
-    Buf xq, sx, h, hq, sh, y, red_out, meta, tbl, rdesc;
+    Buf xq, sx, h, hq, sh, y, meta, tbl, rdesc;
     Buf pin_x, pin_y, pin_meta;
     hipEvent_t ev[N_EVENTS] = {};
     hipEvent_t phase_ev[4] = {};   // expert_group phases under profiling: H2D | kernels | D2H
@@ -357,7 +357,7 @@ void graph_cache_clear(Ctx *c) {
 
 void free_ctx(Ctx *c) {
     graph_cache_clear(c);
-    Buf *dev[] = {&c->xq, &c->sx, &c->h, &c->hq, &c->sh, &c->y, &c->red_out, &c->meta, &c->tbl, &c->rdesc};
+    Buf *dev[] = {&c->xq, &c->sx, &c->h, &c->hq, &c->sh, &c->y, &c->meta, &c->tbl, &c->rdesc};
     for (Buf *b : dev) {
         if (b->p) hipFree(b->p);
         *b = Buf{};
@@ -665,8 +665,9 @@ struct DispatchOpts {
     hipEvent_t after_quant = nullptr;   // recorded after the activation quantisation (profiling)
 };
 
-// The kernel sequence of one dispatch after the activations are on the
-// device: quantise x, gate/up (+SwiGLU), [quantise h], down.
+// The kernel sequence of one dispatch: quantise x (device memory, or mapped
+// host memory for the host-buffer calls), gate/up (+SwiGLU), [quantise h],
+// down.
 void run_experts(Ctx *c, Prof &prof, const ExpertDesc *desc, const RowPlan &plan, const MatGeom &gg,
                  const MatGeom &gd, const float *x_dev, int rows_x, bool x_identity, int R_bound, int T_bound,
                  int ga, int arm, const Scratch &s, const DispatchOpts &opt = DispatchOpts()) {
