@@ -13,9 +13,10 @@ namespace phip {
 // Activation quantisation: qrow_i8 (peregrine-kernels/src/quant.rs:14-33) per
 // row (ACT_ROW) or per 32-element block (ACT_B32). One 256-thread workgroup per
 // row. Output bytes go to the permuted device layout (perm8) and the row is
-// zero-padded to Kp, so padded weight columns contribute nothing.
+// zero-padded to Kp, so padded weight columns contribute nothing. A host-
+// buffer call's kernels also stage its metadata from mapped host memory
+// (a.copy_*), spread over the grid.
 // ---------------------------------------------------------------------------
-// a.copy_n16 words from a.copy_src to a.copy_dst, spread over the grid
 __device__ __forceinline__ void quant_side_copy(const QuantArgs &a) {
     if (a.copy_n16 <= 0) return;
     const int nwg = (int)(gridDim.x * gridDim.y), wg = (int)(blockIdx.y * gridDim.x + blockIdx.x);
