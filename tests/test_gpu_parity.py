@@ -864,6 +864,32 @@ def test_prefill_layer_cfg4_sampled(hip, orc):
     assert np.array_equal(out[sub], ref[sub]), nerr(out[sub], ref[sub])
 
 
+@pytest.mark.parametrize("cfg", ["cfg4", "cfg5"])
+def test_full_size_duplicate_tokens_agree(hip, orc, cfg):
+    """A size-independent property over every token at full size: the second
+    half of the batch repeats the first (same x, same logits), so each token
+    and its copy take the same experts in the same order. Their rows sit at
+    other positions of other M tiles (the copies extend every expert's row
+    range), yet every output must agree bit for bit, and a sample of tokens
+    must equal the oracle."""
+    say("full-size duplicates", cfg)
+    if cfg == "cfg4":
+        E, D, I, S, n_dist, zipf = 160, 5120, 1536, 2048, 24, True
+    else:
+        E, D, I, S, n_dist, zipf = 256, 6144, 2048, 512, 16, False
+    gpu, ora, eset, x, logits = _aliased_case(hip, orc, qt.FMT_I4G, 9000 + S, E, D, I, S, n_dist, zipf)
+    h = S // 2
+    x[h:] = x[:h]
+    logits[h:] = logits[:h]
+    out, ids, w = _run_layer(hip, eset, x, logits, 8, 32, -1)
+    assert np.array_equal(ids[:h], ids[h:])
+    assert np.array_equal(out[:h], out[h:])
+    assert np.all(np.isfinite(out))
+    sub = np.array([0, h - 1, h, S - 1])
+    ref = orc.moe_forward(x, ids, w, ora, 32, subset=sub, nthreads=8)
+    assert np.array_equal(out[sub], ref[sub]), nerr(out[sub], ref[sub])
+
+
 def test_device_exp_equals_glibc_through_the_routers(hip, orc):
     """The kernels' exp (expf_glibc) against glibc's expf, through the two
     routers. Softmax: the top logit is 0 and the other 15 kept logits are the
