@@ -76,6 +76,45 @@ def test_noalloc_decode_shape_and_limit(hip):
         _run(hip, hip.moe_forward_dev_noalloc, eset, x, ids, w, k, 32, -1)
 
 
+def test_noalloc_replayed_from_a_graph(hip):
+    """What the entry point is for: a layer captured into a HIP graph with
+    no allocation anywhere, replayed with new contents written into the same
+    device buffers between replays; every replay equals the allocating entry
+    point run eagerly on those contents."""
+    say("no-alloc graph replay")
+    rng = np.random.default_rng(6144)
+    E, D, I, k, S = 24, 1024, 512, 8, 24
+    _, eset = _layer(hip, rng, E, D, I)
+    bx, bi, bw = hip.DeviceBuffer(S * D * 4), hip.DeviceBuffer(S * k * 4), hip.DeviceBuffer(S * k * 4)
+    bout = hip.DeviceBuffer(S * D * 4)
+
+    def contents():
+        x = rng.standard_normal((S, D)).astype(np.float32)
+        ids, w = synth_route(rng, S, E, k)
+        bx.upload(x)
+        bi.upload(ids)
+        bw.upload(w)
+        return x, ids, w
+
+    def body():
+        hip.moe_forward_dev_noalloc(eset, bx.ptr, S, bi.ptr, bw.ptr, k, bout.ptr, 32, -1)
+
+    x, ids, w = contents()
+    body()   # one eager call first, as for any captured layer
+    hip.pipe_sync(0)
+    # the allocating reference calls below reserve their scratch now, before
+    # the capture (a later growth would make graph_launch refuse the graph)
+    _run(hip, hip.moe_forward_dev, eset, x, ids, w, k, 32, -1)
+    g = hip.capture(0, body)
+    for rep in range(3):
+        x, ids, w = contents()
+        g.launch()
+        hip.pipe_sync(0)
+        got = bout.download(np.float32, (S, D))
+        want = _run(hip, hip.moe_forward_dev, eset, x, ids, w, k, 32, -1)
+        assert np.array_equal(got, want), rep
+
+
 def synth_route(rng, S, E, k):
     logits = synth.normal_logits(rng, S, E)
     order = np.argsort(-logits, axis=1, kind="stable")[:, :k].astype(np.int32)
