@@ -96,8 +96,9 @@ int coli_hip_expert_group_reduce(ColiHipTensor *const *gates, ColiHipTensor *con
  * With COLI_HIP_GRAPH=1 (or the reference's COLI_CUDA_GRAPH=1) in the
  * environment, expert_group* calls are captured once per launch shape (arm,
  * expert count, widths, rows per expert, reduce rows, formats) and replayed;
- * descriptors and activations reach the graph through pinned staging that the
- * replay copies, so a replay uses the current experts and inputs. Not cached:
+ * descriptors and activations reach the graph through mapped host staging
+ * that the replayed kernels read (and the output is written back the same
+ * way), so a replay uses the current experts and inputs. Not cached:
  * calls under profiling or with the debug-dot hook set (graph_cache_stats
  * counts them as uncacheable). */
 int coli_hip_graph_begin(int device);                             /* coli_cuda_graph_begin */
