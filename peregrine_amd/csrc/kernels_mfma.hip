@@ -20,8 +20,11 @@
 #include <cstdlib>
 
 #include "common.h"
+#include "mfma_map.h"
 
 namespace phip {
+
+static_assert(mmap::TILE_O == TILE_O && mmap::BLK == BLK && mmap::MT_ROWS == MT_ROWS, "mfma_map.h geometry");
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -331,33 +334,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATEUP || !
     if (tile >= a.plan.counts[1]) return;
     const int e = a.plan.mt_exp[tile], r0 = a.plan.mt_row0[tile], rend = a.plan.mt_rend[tile];
     const int j = lane & 31, hh = lane >> 5;
-    const int n0 = GATEUP ? ((int)blockIdx.x * 4 + wave) * 32 : ((int)blockIdx.x * 4 + wave) * 32 * NSUB;
+    const int n0 = mmap::dma_n0(GATEUP, (int)blockIdx.x, wave);
     const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_u8);
     float *sxl = (float *)(lds_u8 + (size_t)NSTG * ST::BYTES);   // EPI_B32: [nb][32] activation scales
 
     // copy sources of this lane: a dword of A (row 8*wave + lane/8), its
     // weights (subtile lane/32, column lane%32) and their scales; rows past
     // the expert's end repeat its last row (never stored)
-    int ra = r0 + 8 * wave + (lane >> 3);
-    if (ra >= rend) ra = rend - 1;
+    const int ra = mmap::a_row(r0, rend, wave, lane);
     const uint8_t *src_a = (const uint8_t *)a.xq +
-                           (size_t)(a.act_identity ? ra : a.plan.row_act[ra]) * a.x_stride + (lane & 7) * 4;
-    const int sl = lane >> 5;
-    int oc_l = GATEUP ? n0 + j : n0 + sl * 32 + j;
-    if (oc_l >= g.Op) oc_l = g.Op - 1;
-    const int mat_l = GATEUP ? sl : 2;
+                           (size_t)(a.act_identity ? ra : a.plan.row_act[ra]) * a.x_stride + mmap::a_col(lane);
+    const int oc_l = mmap::dma_ch(GATEUP, n0, lane, g.Op);
+    const int mat_l = mmap::dma_mat(GATEUP, lane);
     const uint8_t *src_w = nullptr;
-    if constexpr (W4) src_w = a.desc[e].w[mat_l] + ((size_t)(oc_l / TILE_O) * g.nb * TILE_O + (oc_l % TILE_O)) * BB;
-    const float *src_s = a.desc[e].sc[mat_l] + (size_t)(oc_l / TILE_O) * g.ng * TILE_O + (oc_l % TILE_O);
+    if constexpr (W4) src_w = a.desc[e].w[mat_l] + mmap::dma_w4(oc_l, g.nb);
+    const float *src_s = a.desc[e].sc[mat_l] + mmap::dma_s(oc_l, g.ng);
     const uint8_t *src_w8[2] = {nullptr, nullptr};
     if constexpr (!W4) {
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            int o = GATEUP ? n0 + (lane >> 1) : n0 + q * 32 + (lane >> 1);
-            if (o >= g.Op) o = g.Op - 1;
-            const int mat = GATEUP ? q : 2;
-            src_w8[q] = a.desc[e].w[mat] + ((size_t)(o / TILE_O) * g.nb * TILE_O + (o % TILE_O)) * BB + (lane & 1) * 16;
-        }
+        for (int q = 0; q < 2; ++q)
+            src_w8[q] = a.desc[e].w[GATEUP ? q : 2] + mmap::dma_w8(mmap::dma_ch8(GATEUP, n0, lane, q, g.Op), g.nb, lane);
     }
     auto copy_blk = [&](int b) {
         const int bc = b < g.nb ? b : g.nb - 1;
@@ -384,14 +380,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATEUP || !
     // waits on them before block 0's wait, which covers them (a wave's loads
     // complete in order). Rows past the tile's end repeat its last row.
     if constexpr (EPI == EPI_B32) {
-        int rx = r0 + (lane & 31);
-        if (rx >= rend) rx = rend - 1;
+        const int rx = mmap::sx_row(r0, rend, lane);
         const float *srcx = a.sx + (size_t)(a.act_identity ? rx : a.plan.row_act[rx]) * a.sx_stride;
         const uint32_t sx_lds = lds_addr + (uint32_t)(NSTG * ST::BYTES);
-        for (int i = wave; i < (g.nb + 1) >> 1; i += 4) {
-            const int b = min(2 * i + (lane >> 5), g.nb - 1);
-            lds_dma4(srcx + b, sx_lds + (uint32_t)(i * 256));
-        }
+        for (int i = wave; i < (g.nb + 1) >> 1; i += 4)
+            lds_dma4(srcx + mmap::sx_blk(i, lane, g.nb), sx_lds + (uint32_t)(i * 256));
     }
 #pragma unroll
     for (int u = 0; u < PD; ++u)
@@ -619,24 +612,18 @@ __global__ __launch_bounds__(256) void mfma_sa_kernel(DotArgs a, MatGeom g) {
     // items [NS * ts, NS * (ts + nt)).
     int tile = blockIdx.y, slab = blockIdx.x;
     if constexpr (XO) {
-        constexpr int XO_G = 8;
-        const int T = a.plan.counts[1], NS = (int)gridDim.x, n = NS * T;
-        const int L = slab + NS * (int)blockIdx.y, chunk = (n + 7) >> 3;
-        const int seq = L >> 3, item = (L & 7) * chunk + seq;
-        if (seq >= chunk || item >= n) return;
+        const int T = a.plan.counts[1], NS = (int)gridDim.x;
+        const int item = mmap::xo_item(slab + NS * (int)blockIdx.y, NS * T);
+        if (item < 0) return;
         const int q = item / NS;                 // a tile of the item's expert
         const int ts = a.plan.mt_first[q];
         const int nt = (a.plan.mt_rend[q] - a.plan.mt_row0[ts] + MT_ROWS - 1) / MT_ROWS;
-        const int local = item - NS * ts;
-        const int grp = local / (NS * XO_G), within = local - grp * NS * XO_G;
-        const int gsize = min(XO_G, nt - grp * XO_G);
-        slab = within / gsize;
-        tile = ts + grp * XO_G + (within - slab * gsize);
+        mmap::xo_place(item, NS, ts, nt, &slab, &tile);
     }
     if (tile >= a.plan.counts[1]) return;
     const int e = a.plan.mt_exp[tile], r0 = a.plan.mt_row0[tile], rend = a.plan.mt_rend[tile];
     const int j = lane & 31, hh = lane >> 5;
-    const int n0 = GATEUP ? (slab * 4 + wave) * 32 : (slab * 4 + wave) * 32 * NSUB;
+    const int n0 = mmap::dma_n0(GATEUP, slab, wave);
     const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_u8);
     float *sxl = (float *)(lds_u8 + (size_t)NSTG * ST::BYTES);   // EPI_B32: [nb][32] activation scales
     auto act_row = [&](int r) { return a.act_identity ? r : a.plan.row_act[r]; };
@@ -644,33 +631,25 @@ __global__ __launch_bounds__(256) void mfma_sa_kernel(DotArgs a, MatGeom g) {
     // ---- copy sources: uniform bases + per-lane offsets ----
     // A: a dword of row 8*wave + lane/8 (rows past the expert's end repeat
     // its last row; never stored)
-    int ra = r0 + 8 * wave + (lane >> 3);
-    if (ra >= rend) ra = rend - 1;
-    const uint32_t voff_a = (uint32_t)act_row(ra) * (uint32_t)a.x_stride + (uint32_t)(lane & 7) * 4;
+    const uint32_t voff_a = (uint32_t)act_row(mmap::a_row(r0, rend, wave, lane)) * (uint32_t)a.x_stride + mmap::a_col(lane);
     const uint8_t *base_a = uniform_ptr(a.xq);
     // weights and their scales: this wave's two subtiles 2w, 2w+1 (one
     // tensor), lane half hh -> subtile 2w + hh; tiles past the tensor clamp
     // to its last tile (never stored)
-    const int mat = GATEUP ? (wave >> 1) : 2;
+    const int mat = mmap::sa_mat(GATEUP, wave);
     const int ntile = g.Op / TILE_O;
-    int wt = GATEUP ? slab * 4 + 2 * (wave & 1) + hh : slab * 8 + 2 * wave + hh;
-    if (wt >= ntile) wt = ntile - 1;
     const uint8_t *base_w = uniform_ptr(a.desc[e].w[mat]);
     const uint8_t *base_s = uniform_ptr(a.desc[e].sc[mat]);
-    const uint32_t tile_w = (uint32_t)g.nb * ST::SUB;
     uint32_t voff_w;
-    if constexpr (W4) voff_w = (uint32_t)wt * tile_w + (uint32_t)j * 16;
-    else voff_w = (uint32_t)(lane >> 1) * 32 + (uint32_t)(lane & 1) * 16;   // int8: one subtile per copy
+    if constexpr (W4) voff_w = mmap::sa_voff_w4(GATEUP, slab, wave, lane, ntile, g.nb);
+    else voff_w = mmap::sa_voff_w8(lane);   // int8: one subtile per copy
     uint32_t tile_w8[2] = {0, 0};
     if constexpr (!W4) {
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            int t = GATEUP ? slab * 4 + 2 * (wave & 1) + q : slab * 8 + 2 * wave + q;
-            if (t >= ntile) t = ntile - 1;
-            tile_w8[q] = __builtin_amdgcn_readfirstlane((uint32_t)t * tile_w);
-        }
+        for (int q = 0; q < 2; ++q)
+            tile_w8[q] = __builtin_amdgcn_readfirstlane(mmap::sa_tile8(GATEUP, slab, wave, q, ntile, g.nb));
     }
-    const uint32_t voff_s = (uint32_t)wt * (uint32_t)g.ng * 128 + (uint32_t)j * 4;
+    const uint32_t voff_s = mmap::sa_voff_s(GATEUP, slab, wave, lane, ntile, g.ng);
 
     auto copy_blk = [&](int b, int stg) {
         const uint32_t st = lds_addr + (uint32_t)(stg * ST::BYTES);
@@ -694,14 +673,10 @@ __global__ __launch_bounds__(256) void mfma_sa_kernel(DotArgs a, MatGeom g) {
     // one copy per wave covers two blocks of the 32 rows; block 0's wait
     // covers them (a wave's loads complete in order)
     if constexpr (EPI == EPI_B32) {
-        int rx = r0 + (lane & 31);
-        if (rx >= rend) rx = rend - 1;
-        const float *srcx = a.sx + (size_t)act_row(rx) * a.sx_stride;
+        const float *srcx = a.sx + (size_t)act_row(mmap::sx_row(r0, rend, lane)) * a.sx_stride;
         const uint32_t sx_lds = lds_addr + (uint32_t)(NSTG * ST::BYTES);
-        for (int i = wave; i < (g.nb + 1) >> 1; i += 4) {
-            const int b = min(2 * i + (lane >> 5), g.nb - 1);
-            lds_dma4(srcx + b, sx_lds + (uint32_t)(i * 256));
-        }
+        for (int i = wave; i < (g.nb + 1) >> 1; i += 4)
+            lds_dma4(srcx + mmap::sx_blk(i, lane, g.nb), sx_lds + (uint32_t)(i * 256));
     }
 #pragma unroll
     for (int u = 0; u < PD; ++u)
@@ -883,9 +858,7 @@ static size_t mfma_sa_lds(const MatGeom &g) {
 
 template <bool W4, int EPI, bool GATEUP, int PD, bool WNT, bool XO = false>
 static void launch_mfma_sa_h(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
-    const int ch_per_wg = GATEUP ? 4 * 32 : 4 * 32 * 2;
-    const int span = GATEUP ? ((g.O + 31) & ~31) : g.O;
-    dim3 grid((unsigned)((span + ch_per_wg - 1) / ch_per_wg), (unsigned)grid_tiles);
+    dim3 grid((unsigned)mmap::slab_count(GATEUP, g.O), (unsigned)grid_tiles);
     const size_t lds = mfma_sa_lds<W4, EPI, PD>(g);
     auto kern = mfma_sa_kernel<W4, EPI, GATEUP, PD, WNT, XO>;
     static size_t opted[LDS_OPT_DEVICES];
@@ -920,9 +893,7 @@ constexpr int DMA_PD_SHALLOW = 3, DMA_PD_NARROW = 2, DMA_PD_DEEP_W4 = 6, DMA_PD_
 template <bool W4, int EPI, bool GATEUP, int PD, bool WNT>
 static void launch_mfma_dma_h(const DotArgs &a, const MatGeom &g, int grid_tiles, hipStream_t st) {
     constexpr int NSUB = 2;
-    const int ch_per_wg = GATEUP ? 4 * 32 : 4 * 32 * NSUB;
-    const int span = GATEUP ? ((g.O + 31) & ~31) : g.O;
-    dim3 grid((unsigned)((span + ch_per_wg - 1) / ch_per_wg), (unsigned)grid_tiles);
+    dim3 grid((unsigned)mmap::slab_count(GATEUP, g.O), (unsigned)grid_tiles);
     const size_t lds = mfma_dma_lds<W4, EPI, PD>(g);
     auto kern = mfma_dma_kernel<W4, EPI, GATEUP, NSUB, PD, WNT>;
     static size_t opted[LDS_OPT_DEVICES];

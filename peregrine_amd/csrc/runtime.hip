@@ -764,37 +764,48 @@ bool graph_cache_enabled() {
     return v && std::atoi(v) != 0;
 }
 
+// A call's launch shape: fixed fields, then rows per expert (at most 256).
+// Built on the stack per call; a slot copies it only when a graph is stored.
+constexpr int SHAPE_FIELDS = 11, SHAPE_MAX = SHAPE_FIELDS + 256;
 struct ShapeKey {
-    std::vector<int> v;
+    int n = 0;
+    int v[SHAPE_MAX];
     uint64_t hash = 0;
 };
 
-ShapeKey shape_key(const std::vector<int> &fields, const int *rows, int count) {
-    ShapeKey k;
-    k.v = fields;
-    k.v.insert(k.v.end(), rows, rows + count);
+void shape_key(ShapeKey *k, const int (&fields)[SHAPE_FIELDS], const int *rows, int count) {
+    k->n = SHAPE_FIELDS + count;
+    std::memcpy(k->v, fields, sizeof(fields));
+    std::memcpy(k->v + SHAPE_FIELDS, rows, (size_t)count * sizeof(int));
     uint64_t h = 0xcbf29ce484222325ull;   // FNV-1a, 64-bit
-    for (int x : k.v)
+    for (int i = 0; i < k->n; i++)
         for (int b = 0; b < 4; b++) {
-            h ^= (uint64_t)((uint32_t)x >> (8 * b)) & 0xff;
+            h ^= (uint64_t)((uint32_t)k->v[i] >> (8 * b)) & 0xff;
             h *= 0x100000001b3ull;
         }
-    k.hash = h;
-    return k;
+    k->hash = h;
 }
 
 std::vector<int> g_slot_shape[COLI_HIP_MAX_DEVICES][GRAPH_CACHE];
+
+bool slot_shape_is(const std::vector<int> &s, const ShapeKey &key) {
+    return (int)s.size() == key.n && std::memcmp(s.data(), key.v, (size_t)key.n * sizeof(int)) == 0;
+}
+
+void drop_slot(GraphSlot &sl) {   // a graph whose baked scratch addresses are stale
+    graph_destroy(sl.g);
+    sl = GraphSlot{};
+    std::lock_guard<std::mutex> lock(g_stats_mu);
+    g_graph_invalidations++;
+}
 
 ColiHipGraph *graph_lookup(Ctx *c, const ShapeKey &key) {
     const int ci = (int)(c - g_ctx);
     for (int i = 0; i < GRAPH_CACHE; i++) {
         GraphSlot &sl = c->graphs[i];
-        if (!sl.g || sl.key != key.hash || g_slot_shape[ci][i] != key.v) continue;
+        if (!sl.g || sl.key != key.hash || !slot_shape_is(g_slot_shape[ci][i], key)) continue;
         if (sl.gen != c->gen) {   // scratch moved since the capture
-            graph_destroy(sl.g);
-            sl = GraphSlot{};
-            std::lock_guard<std::mutex> lock(g_stats_mu);
-            g_graph_invalidations++;
+            drop_slot(sl);
             return nullptr;
         }
         sl.used = ++c->graph_clock;
@@ -805,6 +816,10 @@ ColiHipGraph *graph_lookup(Ctx *c, const ShapeKey &key) {
 
 void graph_store(Ctx *c, const ShapeKey &key, ColiHipGraph *g) {
     const int ci = (int)(c - g_ctx);
+    // graphs captured before a scratch reallocation can never replay: free
+    // them (and their exec resources) before choosing an LRU victim
+    for (int i = 0; i < GRAPH_CACHE; i++)
+        if (c->graphs[i].g && c->graphs[i].gen != c->gen) drop_slot(c->graphs[i]);
     int victim = 0;
     for (int i = 0; i < GRAPH_CACHE; i++) {
         if (!c->graphs[i].g) {
@@ -819,7 +834,7 @@ void graph_store(Ctx *c, const ShapeKey &key, ColiHipGraph *g) {
     sl.g = g;
     sl.gen = c->gen;
     sl.used = ++c->graph_clock;
-    g_slot_shape[ci][victim] = key.v;
+    g_slot_shape[ci][victim].assign(key.v, key.v + key.n);
 }
 
 int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, ColiHipTensor *const *downs,
@@ -965,8 +980,8 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
     const bool graphs_on = graph_cache_enabled();
     if (graphs_on && !profile && !g_dbg_gu && !g_dbg_dn) {
         const ColiHipTensor *g0 = gates[0], *d0 = downs[0];
-        const ShapeKey key = shape_key({arm, count, D, gg.O, s_n, ga, g0->fmt, g0->gs, d0->fmt, d0->gs, g_spin_limit},
-                                       rows, count);
+        ShapeKey key;
+        shape_key(&key, {arm, count, D, gg.O, s_n, ga, g0->fmt, g0->gs, d0->fmt, d0->gs, g_spin_limit}, rows, count);
         ColiHipGraph *g = graph_lookup(c, key);
         if (!g) {
             Prof off(c);

@@ -48,13 +48,15 @@ def test_expf_glibc_equals_libm_on_every_f32(sweep_bin):
 def test_double_rounded_exp_differs_from_glibc():
     """The construction used before, exp in double rounded once to f32,
     differs from glibc's expf on a measurable share of inputs (170,648 of the
-    2^32 patterns on this host's glibc; 131 of this fixed sample of 200,000
-    in [-20, 20], where SiLU's and the router's arguments lie)."""
+    2^32 patterns on the glibc this was first measured on; 131 of this fixed
+    sample of 200,000 in [-20, 20], where SiLU's and the router's arguments
+    lie). The exact count depends on the glibc build, so only its presence
+    and its rarity are asserted."""
     xs = np.random.default_rng(0).uniform(-20, 20, 200000).astype(np.float32)
     dbl = np.array([_libm.exp(float(v)) for v in xs], np.float64).astype(np.float32)
     gl = np.array([_libm.expf(float(v)) for v in xs], np.float32)
     n = int(np.sum(dbl.view(np.uint32) != gl.view(np.uint32)))
-    assert n == 131, n
+    assert 0 < n <= 0.01 * len(xs), n
 
 
 def test_oracle_silu_is_glibc_expf(orc):

@@ -147,6 +147,49 @@ def test_expert_group_reduce(hip, orc, ga):
     assert np.array_equal(out, hip.expert_group_reduce(gpu, rows, x, D, lay, rw, 2))
 
 
+@pytest.mark.parametrize("rows", [[96], [70, 70, 5], [64] * 5])
+@pytest.mark.parametrize("fmt,gs", [(qt.FMT_I4G, 32), (qt.FMT_I4, 0)])
+@pytest.mark.parametrize("ga", [0, 32])
+@pytest.mark.parametrize("graph", [0, 1])
+def test_expert_group_weight_reuse_shapes(hip, orc, rows, fmt, gs, ga, graph):
+    """int4 expert_group / expert_group_reduce shapes with two or more M tiles
+    per expert (the weight-reuse dispatch, XCD-ordered work items) and a grid
+    of exactly the M tiles: odd tile counts, 5 experts x 2 tiles, eager and
+    through the graph cache, bit-identical to the oracle. The mapped output
+    staging buffer is shared by every call, so an unwritten slab would return
+    an earlier call's values and fail the comparison."""
+    import os
+    say("expert_group weight reuse", rows, fmt, gs, ga, graph)
+    rng = np.random.default_rng(0x5EED + sum(rows) + fmt + ga + graph)
+    D, I = 1536, 640   # gate/up: 5 slabs of 128 channels; down: 6 slabs of 256
+    gpu, ora = _experts(rng, len(rows), D, I, fmt, gs or 32, orc, hip)
+    R = sum(rows)
+    x = rng.standard_normal((R, D)).astype(np.float32)
+    dst = rng.integers(0, 7, R).astype(np.int32)
+    rw = rng.uniform(0.1, 1.0, R).astype(np.float32)
+    lay = hip.ReduceLayout.build(dst, 7)
+    hip.set_act_group(ga)
+    hip.set_arm(2)
+    old = os.environ.get("COLI_HIP_GRAPH")
+    os.environ["COLI_HIP_GRAPH"] = str(graph)
+    offs = np.concatenate([[0], np.cumsum(rows)])
+    ref = np.concatenate([orc.expert_swiglu(x[offs[e]:offs[e + 1]], *ora[e], ga) for e in range(len(rows))])
+    ref_out = orc.grouped_reduce(ref, lay.row_ptr, lay.row_idx, rw, 7)
+    try:
+        for _ in range(2):   # graph: capture, then replay
+            y = hip.expert_group(gpu, rows, x, D)
+            for e in range(len(rows)):
+                a, b = offs[e], offs[e + 1]
+                assert np.array_equal(y[a:b], ref[a:b]), f"expert {e}: not bit-identical, err {nerr(y[a:b], ref[a:b])}"
+            assert np.array_equal(hip.expert_group_reduce(gpu, rows, x, D, lay, rw, 7), ref_out)
+    finally:
+        hip.set_arm(-1)
+        if old is None:
+            os.environ.pop("COLI_HIP_GRAPH", None)
+        else:
+            os.environ["COLI_HIP_GRAPH"] = old
+
+
 def test_expert_group_error_paths(hip, orc):
     say("error paths")
     rng = np.random.default_rng(3)

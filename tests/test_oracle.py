@@ -222,9 +222,9 @@ def test_silu_closed_form(orc):
         assert abs(got - exact) <= 2 * np.spacing(np.float32(abs(exact)) + np.float32(1e-30))
 
 
-def test_silu_matches_glibc_expf_almost_always(orc):
-    # the oracle's exp is correctly rounded; Rust's f32::exp (glibc expf)
-    # differs only near rounding midpoints. Measure that it is rare.
+def test_silu_matches_glibc_expf_exactly(orc):
+    # the oracle's SiLU calls glibc's expf, which is what Rust's f32::exp
+    # (math.rs:108-111) calls on Linux: no input may differ.
     import ctypes
     libm = ctypes.CDLL("libm.so.6")
     libm.expf.restype = ctypes.c_float
@@ -234,7 +234,7 @@ def test_silu_matches_glibc_expf_almost_always(orc):
     for v in xs:
         ref = np.float32(v / np.float32(np.float32(1.0) + np.float32(libm.expf(float(-v)))))
         diff += ref.tobytes() != orc.silu(v).tobytes()
-    assert diff <= 0.01 * len(xs)
+    assert diff == 0
 
 
 def test_expert_swiglu_tracks_f64(orc):
