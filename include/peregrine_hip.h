@@ -148,6 +148,17 @@ int coli_hip_set_fused_route(int mode);
  * eligible. COLI_HIP_FUSED_COMBINE=0 or =1 in the environment sets 0 or 1 at
  * first use. */
 int coli_hip_set_fused_combine(int mode);
+/* Split-K GEMV arm (NEW, no counterpart in backend_cuda.h): the K blocks of
+ * each (row, output tile) are spread over several workgroups so that decode
+ * launches cover the chip; the workgroup that finishes a tile's count runs
+ * its exact f32 chain, so results are the same bits as the unsplit kernel.
+ * target_wgs is the workgroup count a GEMV launch aims for; 0 never splits
+ * (the default: on MI355X the hand-off between workgroups costs more than the
+ * extra CUs gain at the BASELINE decode shapes); -1 restores the default.
+ * COLI_HIP_GEMV_SPLIT=<n> in the environment sets it at first use. A split gate/up GEMV takes the router launch apart (the fused
+ * router prologue runs in the unsplit kernel only), and in automatic mode a
+ * split down projection combines in its tail instead of the fused kernel. */
+int coli_hip_set_gemv_split(int target_wgs);
 
 /* ---- NEW: device-resident MoE layer (inputs already in HBM) ---- */
 /* A fixed expert table: expert id e -> (gates[e], ups[e], downs[e]). */

@@ -64,6 +64,7 @@ SIGNATURES = {
     "coli_hip_set_arm": (_i, [_i]),
     "coli_hip_set_fused_route": (_i, [_i]),
     "coli_hip_set_fused_combine": (_i, [_i]),
+    "coli_hip_set_gemv_split": (_i, [_i]),
     "coli_hip_expert_set_create": (_i, [C.POINTER(_p), _p, _p, _p, _i]),
     "coli_hip_expert_set_free": (None, [_p]),
     "coli_hip_route_softmax_topk_dev": (_i, [_i, _p, _i, _i, _i, _p, _p]),

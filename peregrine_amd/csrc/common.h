@@ -124,6 +124,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, ui
 // hint (cache-policy bit 1), which on gfx950 doubles the rate of a streaming
 // read against plain loads that allocate in the caches.
 constexpr int BUF_NT = 2;
+// Cache-policy bit SC1 (device scope on gfx942/gfx950): the same encoding the
+// compiler gives agent-scope atomic loads and stores, i.e. coherent across
+// the XCDs' L2s, but as plain operations the compiler may batch.
+constexpr int BUF_SC1 = 16;
 __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, BUF_NT);
     return make_uint4(v[0], v[1], v[2], v[3]);
@@ -268,10 +272,30 @@ struct DotArgs {   // shared by the GEMV and MFMA arms
     float *tail_out;
     const float *tail_w;
     int *tail_ctr;
+    // split-K GEMV (split > 1): each (row, output tile) unit's K blocks are
+    // spread over `split` workgroups of split_kb blocks each; they park their
+    // exact block dots and f32 factors in part_d / part_f and count in on
+    // split_ctr[unit] (zero between dispatches); the last to arrive runs the
+    // unit's ascending f32 chain and its epilogue
+    int split, split_kb, split_nw;
+    int32_t *part_d;
+    float *part_f;
+    int *split_ctr;
 };
 // output tiles the tail counters cover (down GEMV tiles are 64 channels)
 constexpr int GEMV_TAIL_TILES = 4096;
 constexpr int GEMV_TAIL_MAXK = 16;
+// split-K GEMV: arrival counters (units = rows x output tiles) and the most
+// blocks one wave of the finishing workgroup holds for the chain
+constexpr int GEMV_SPLIT_UNITS = 16384;
+constexpr int GEMV_SPLIT_SEG = 24;
+// Split-K plan of one GEMV launch: 0 = the unsplit kernel. Fills split /
+// split_kb of a DotArgs and returns the partial-buffer bytes it needs.
+struct GemvSplit {
+    int split = 0, kb = 0, nw = 0, ch = 0;
+    size_t part_d_bytes = 0, part_f_bytes = 0;
+};
+GemvSplit plan_gemv_split(const MatGeom &g, bool gateup, int rows, int act, int target_wgs);
 // grid_rows / grid_tiles: host-side upper bounds; the kernels read the true
 // counts from plan.counts and idle the excess workgroups.
 void launch_gemv_gateup(const DotArgs &a, const MatGeom &g, int act, int grid_rows, hipStream_t st);

@@ -12,6 +12,7 @@
 // Streaming waves turn blocks into (integer dot, f32 factor) pairs in an LDS
 // ring; one chain wave applies them in ascending block order. Integer dots
 // are exact whatever the split.
+#include <algorithm>
 #include <cstdlib>
 
 #include "common.h"
@@ -92,11 +93,11 @@ __device__ __forceinline__ void spin_until_geq(int *ctr, int target, int limit, 
 // (write-through / coherent reads of just those lines), the stores have
 // completed (vmcnt 0) before the count is incremented, the count is an
 // agent-scope read-modify-write, and the loads issue only after it returns.
-__device__ __forceinline__ void tail_combine(const DotArgs &a, int O, int nrows, int o) {
+__device__ __forceinline__ void tail_combine(const DotArgs &a, int O, int nrows, int o, int tile) {
     const int lane = threadIdx.x & 63;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     int old = 0;
-    if (lane == 0) old = __hip_atomic_fetch_add(&a.tail_ctr[blockIdx.x], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) old = __hip_atomic_fetch_add(&a.tail_ctr[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     old = __shfl(old, 0);
     if (old != nrows - 1) return;   // uniform
     asm volatile("" ::: "memory");
@@ -113,7 +114,7 @@ __device__ __forceinline__ void tail_combine(const DotArgs &a, int O, int nrows,
     for (int j = 0; j < GEMV_TAIL_MAXK; ++j)
         if (j < nrows) acc = __fadd_rn(acc, __fmul_rn(wv[j], yv[j]));
     if (o < O) a.tail_out[o] = acc;
-    if (lane == 0) __hip_atomic_store(&a.tail_ctr[blockIdx.x], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) __hip_atomic_store(&a.tail_ctr[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // NW streaming waves plus one chain wave. K is walked in rounds of NW*CH
@@ -406,9 +407,247 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemv_kernel(DotArgs a, MatGeom 
             if (o < g.O) a.out[(size_t)r * a.out_stride + o] = v;
         } else {
             if (o < g.O) __hip_atomic_store(&a.out[(size_t)r * a.out_stride + o], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            tail_combine(a, g.O, nrows, o);
+            tail_combine(a, g.O, nrows, o, (int)blockIdx.x);
         }
     }
+}
+
+// ---------------------------------------------------------------------------
+// Split-K decode GEMV. A unit is one row and one output tile (32 gate + 32 up
+// channels, or 64 down channels); its K blocks are spread over `split`
+// workgroups of split_kb blocks, so a one-token layer runs on many more
+// workgroups than it has tiles (config 1's gate/up has 48 tiles for 256 CUs).
+//
+// Streaming: wave w of workgroup s takes blocks s*kb + w*CH + [0, CH), issues
+// its weight, scale and activation loads as one batch and turns each block
+// into its exact integer dot and its f32 factor (sw*sx[b] for 32-block
+// activation scales, sw for grouped weights), exactly as gemv_kernel's
+// streaming waves do. It parks them in part_d / part_f (int4 dots fit 16
+// bits, so two blocks share a dword) and the workgroup counts in on the
+// unit's counter.
+//
+// The chain: the workgroup that completes the count loads the unit's pairs
+// (wave w holds blocks [w*SEG, (w+1)*SEG)) and runs the one ascending f32
+// chain of idot.rs:82-88 over them, wave after wave, handing the running
+// value over through LDS; then the epilogue (SwiGLU and the h quantisation,
+// or the y store and the one-token tail combine). The arithmetic is the
+// unsplit kernel's, step for step, so the bits are too.
+//
+// Visibility across XCDs, the tail combine's scheme: the pairs are written
+// with the device-scope cache policy (SC1, what agent-scope atomic stores
+// compile to: written through the XCD's L2), every wave waits for its stores
+// (vmcnt 0) before the workgroup barrier that precedes the agent-scope
+// counter add, and the finishing workgroup reads the pairs with SC1 loads
+// (coherent reads, as agent-scope atomic loads) issued after the add
+// returned. As plain buffer operations rather than atomics they are issued
+// as one batch: atomic loads were serialised one round trip each (config 1's
+// split down projection took 19 us instead of 5). Nothing waits on another
+// workgroup, so no dispatch order is assumed. The finisher resets the
+// counter to 0 for the next dispatch.
+// ---------------------------------------------------------------------------
+template <bool W4, int EPI, bool GATEUP, int CH>
+__global__ __launch_bounds__(1024) void gemv_split_kernel(DotArgs a, MatGeom g, const int8_t *__restrict__ xq,
+                                                          const float *__restrict__ sxv) {
+    static_assert(CH % 2 == 0, "int4 dots are parked in pairs of blocks");
+    constexpr int BB = W4 ? 16 : 32;
+    constexpr int SEGMAX = GEMV_SPLIT_SEG;
+    __shared__ float hand_f[64];   // the chain's running value between waves
+    __shared__ int hand_i[64];     // and its open integer sum (per-row / grouped weights)
+    __shared__ int is_last;
+
+    const int lane = threadIdx.x & 63, wave = wave_id(), nw = (int)blockDim.x >> 6;
+    const int S = a.split, kb = a.split_kb, nb = g.nb;
+    const int u = (int)blockIdx.x / S, s = (int)blockIdx.x - u * S, r = blockIdx.y;
+    const int nrows = a.n_rows_fixed >= 0 ? a.n_rows_fixed : a.plan.counts[0];
+    if (r >= nrows) return;   // uniform: fewer rows than the grid bound
+    const int ntx = (int)gridDim.x / S;
+    const size_t unit = (size_t)r * ntx + u;
+    const int nbd = W4 ? (nb + 1) >> 1 : nb;   // dwords of parked dots per lane
+    // this unit's parked pairs, [block][64 lanes] (int4 dots: [block pair][64]),
+    // through buffer resources: offsets are lane*4 + block*256
+    const auto rd = make_rsrc(a.part_d + unit * nbd * 64, (uint32_t)nbd * 256);
+    const auto rf = make_rsrc(EPI == EPI_ROW ? (const void *)a.part_d : (const void *)(a.part_f + unit * nb * 64),
+                              (uint32_t)nb * 256);
+    const int lo4 = lane * 4;
+
+    const ExpertDesc *dsc = a.plan.row_desc ? &a.plan.row_desc[r] : &a.desc[a.plan.row_exp[r]];
+    const int arow = a.act_identity ? r : (a.act_zero ? 0 : a.plan.row_act[r]);
+    const int half = lane >> 5, ol = lane & 31;
+    const int o = GATEUP ? u * 32 + ol : u * 64 + lane;
+    const int mat = GATEUP ? half : 2;
+    const int tile = GATEUP ? u : 2 * u + half;
+    const auto *wp = gptr(dsc->w[mat] + ((size_t)tile * nb * TILE_O + ol) * BB);
+    const auto *sp = gptr(dsc->sc[mat] + (size_t)tile * g.ng * TILE_O + ol);
+    const CInt *xs = (const CInt *)(xq + (size_t)arow * a.x_stride);
+    const CFloat *sxs = (const CFloat *)(sxv + (size_t)arow * a.sx_stride);
+
+    // ---- streaming: this wave's CH blocks ----
+    const int bw = s * kb + wave * CH;
+    if (bw < nb) {   // uniform
+        WBlk<W4> wv[CH];
+        float sv[CH];
+        int xr[CH][8];
+        float sxr[CH];
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int b = min(bw + j, nb - 1);
+            wv[j] = load_wblk<W4>((const uint8_t *)(wp + (size_t)b * (TILE_O * BB)));
+            if constexpr (EPI != EPI_ROW) sv[j] = __builtin_nontemporal_load(&sp[(size_t)grp_of(b, g.gshift) * TILE_O]);
+        }
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int b = min(bw + j, nb - 1);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) xr[j][q] = xs[b * (BLK / 4) + q];
+            if constexpr (EPI == EPI_B32) sxr[j] = sxs[b];
+        }
+        int dv[CH];
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int d16 = dot_wblk<W4>(wv[j], xr[j]);
+            dv[j] = W4 ? (d16 >> 4) : d16;   // exact block dot
+            if constexpr (EPI != EPI_ROW) {
+                const float sw = W4 ? __fmul_rn(sv[j], 16.0f) : sv[j];   // W4 scale tables hold sw/16
+                const float f = EPI == EPI_B32 ? __fmul_rn(sw, sxr[j]) : sw;
+                if (bw + j < nb) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(f), rf, lo4 + (bw + j) * 256, 0, BUF_SC1);
+            }
+        }
+        if constexpr (W4) {
+#pragma unroll
+            for (int j = 0; j < CH; j += 2) {
+                const int pk = (int)(((uint32_t)dv[j] & 0xFFFFu) | ((uint32_t)dv[j + 1] << 16));
+                if (bw + j < nb) __builtin_amdgcn_raw_buffer_store_b32((uint32_t)pk, rd, lo4 + ((bw + j) >> 1) * 256, 0, BUF_SC1);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < CH; ++j)
+                if (bw + j < nb) __builtin_amdgcn_raw_buffer_store_b32((uint32_t)dv[j], rd, lo4 + (bw + j) * 256, 0, BUF_SC1);
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's pairs are written through
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int old = __hip_atomic_fetch_add(&a.split_ctr[unit], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        is_last = old == S - 1;
+        if (old == S - 1) __hip_atomic_store(&a.split_ctr[unit], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!is_last) return;   // uniform over the workgroup
+    asm volatile("" ::: "memory");
+
+    // ---- the chain, in the workgroup that completed the count ----
+    const int seg = (((nb + nw - 1) / nw) + 1) & ~1;   // even: int4 pairs never straddle waves
+    const int c0 = wave * seg, n = max(0, min(nb, c0 + seg) - c0);
+    int dd[SEGMAX];
+    float ff[SEGMAX];
+    if constexpr (W4) {
+#pragma unroll
+        for (int i = 0; i < SEGMAX; i += 2) {   // unconditional, clamped: one batch of loads
+            const int bd = min((c0 + i) >> 1, nbd - 1);
+            const int pk = (int)__builtin_amdgcn_raw_buffer_load_b32(rd, lo4 + bd * 256, 0, BUF_SC1);
+            dd[i] = (int)(short)(pk & 0xFFFF);
+            dd[i + 1] = pk >> 16;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < SEGMAX; ++i)
+            dd[i] = (int)__builtin_amdgcn_raw_buffer_load_b32(rd, lo4 + min(c0 + i, nb - 1) * 256, 0, BUF_SC1);
+    }
+#pragma unroll
+    for (int i = 0; i < SEGMAX; ++i)
+        ff[i] = EPI == EPI_ROW ? 0.0f
+                               : __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rf, lo4 + min(c0 + i, nb - 1) * 256, 0,
+                                                                                      BUF_SC1));
+    float facc = 0.0f;
+    int isum = 0;   // EPI_ROW: exact integer sum; EPI_GRP: the open group's sum
+    for (int w = 0; w < nw; ++w) {
+        if (wave == w && (w == 0 || c0 < nb)) {
+            if (w > 0) {
+                facc = hand_f[lane];
+                isum = hand_i[lane];
+            }
+#pragma unroll
+            for (int i = 0; i < SEGMAX; ++i) {
+                if (i >= n) break;   // uniform
+                const int b = c0 + i;
+                if constexpr (EPI == EPI_ROW) {
+                    isum += dd[i];
+                } else if constexpr (EPI == EPI_B32) {
+                    facc = __fmaf_rn(ff[i], (float)dd[i], facc);
+                } else {
+                    isum += dd[i];
+                    if (grp_end(b, g.gshift, nb)) {
+                        facc = __fadd_rn(facc, __fmul_rn((float)isum, ff[i]));
+                        isum = 0;
+                    }
+                }
+            }
+            hand_f[lane] = facc;
+            hand_i[lane] = isum;
+        }
+        __syncthreads();
+    }
+    if (wave != 0) return;
+    facc = hand_f[lane];
+    isum = hand_i[lane];
+    float v;
+    if constexpr (EPI == EPI_ROW) {
+        const float sc = W4 ? __fmul_rn(sp[0], 16.0f) : sp[0];   // per-row scale
+        v = __fmul_rn(__fmul_rn((float)isum, sc), sxs[0]);
+    } else if constexpr (EPI == EPI_GRP) {
+        v = __fmul_rn(facc, sxs[0]);
+    } else {
+        v = facc;
+    }
+    if constexpr (GATEUP) {
+        const float uu = __shfl(v, (lane & 31) + 32);
+        if (lane < 32) {
+            const float h = silu_mul(v, uu);
+            if (!(EPI == EPI_B32 && a.hq)) a.out[(size_t)r * a.out_stride + o] = h;   // else only hq / sh are read
+            if (EPI == EPI_B32 && a.hq) {
+                const float m = warp_max(fabsf(h), 32);
+                float sc = __fdiv_rn(m, 127.0f);
+                if (sc < 1e-12f) sc = 1e-12f;
+                const float inv = __fdiv_rn(1.0f, sc);
+                a.hq[(size_t)r * a.hq_stride + perm8(o)] = (int8_t)(int)rintf(__fmul_rn(h, inv));
+                if ((lane & 31) == 0) a.sh[(size_t)r * a.sh_stride + (o >> 5)] = sc;
+            }
+        }
+    } else {
+        if (!a.tail_out) {
+            if (o < g.O) a.out[(size_t)r * a.out_stride + o] = v;
+        } else {
+            if (o < g.O) __hip_atomic_store(&a.out[(size_t)r * a.out_stride + o], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            tail_combine(a, g.O, nrows, o, u);
+        }
+    }
+}
+
+GemvSplit plan_gemv_split(const MatGeom &g, bool gateup, int rows, int act, int target_wgs) {
+    GemvSplit p;
+    const int ntx = gateup ? (g.O + 31) / 32 : (g.O + 63) / 64;
+    const long units = (long)rows * ntx;
+    if (target_wgs <= 0 || rows < 1 || units > GEMV_SPLIT_UNITS) return p;
+    const int nb = g.nb;
+    int S = (int)std::min<long>(std::max<long>(target_wgs / units, 1), nb);
+    if (S <= 1) return p;
+    int kb = (nb + S - 1) / S;
+    const int ch = kb >= 16 ? 4 : 2;
+    // the finishing workgroup holds at most SEG blocks per wave for the chain
+    const int nw_chain = (nb + GEMV_SPLIT_SEG - 1) / GEMV_SPLIT_SEG;
+    int nw = std::max((kb + ch - 1) / ch, nw_chain);
+    if (nw > 16) return p;
+    kb = nw * ch;
+    S = (nb + kb - 1) / kb;
+    if (S <= 1) return p;
+    p.split = S;
+    p.kb = kb;
+    p.nw = nw;
+    p.ch = ch;
+    p.part_d_bytes = (size_t)units * (g.w4 ? (nb + 1) / 2 : nb) * 64 * 4;
+    const int epi = act == ACT_B32 ? EPI_B32 : (g.per_row ? EPI_ROW : EPI_GRP);
+    p.part_f_bytes = epi == EPI_ROW ? 0 : (size_t)units * nb * 64 * 4;
+    return p;
 }
 
 // One token, down projection and combine in one launch. A workgroup owns 16
@@ -589,6 +828,14 @@ static void launch_gemv_c(const DotArgs &a, const MatGeom &g, int grid_rows, hip
 
 template <bool W4, int EPI, bool GATEUP>
 static void launch_gemv_t(const DotArgs &a, const MatGeom &g, int grid_rows, hipStream_t st) {
+    if (a.split > 1) {
+        const int ntx = GATEUP ? (g.O + 31) / 32 : (g.O + 63) / 64;
+        const int ch = a.split_kb / a.split_nw;
+        const dim3 grid((unsigned)(ntx * a.split), (unsigned)grid_rows), block((unsigned)(64 * a.split_nw));
+        if (ch == 4) launch_k((gemv_split_kernel<W4, EPI, GATEUP, 4>), grid, block, 0, st, a, g, a.xq, a.sx);
+        else launch_k((gemv_split_kernel<W4, EPI, GATEUP, 2>), grid, block, 0, st, a, g, a.xq, a.sx);
+        return;
+    }
     if constexpr (GATEUP) {
         if (a.route.logits) {
             launch_gemv_c<W4, EPI, GATEUP, W4 ? 5 : 4, true>(a, g, grid_rows, st);

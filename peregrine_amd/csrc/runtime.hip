@@ -28,6 +28,9 @@ static __device__ __align__(256) uint8_t scratch[COLI_HIP_FIXED_SCRATCH_BYTES];
 // its counter), so no clearing launch is needed. One stream per device uses
 // them; host code uses the address kept in Ctx::tail_ctr.
 static __device__ int tail_ctr[GEMV_TAIL_TILES];
+// Per-unit arrival counters of the split-K GEMV, kept zero between
+// dispatches the same way (the unit's finishing workgroup resets its own).
+static __device__ int split_ctr[GEMV_SPLIT_UNITS];
 
 namespace {
 struct Slab;
@@ -81,7 +84,7 @@ struct Ctx {
     hipStream_t stream = nullptr;
     size_t tensor_count = 0, tensor_bytes = 0;
     unsigned gen = 0;   // bumped on every scratch reallocation
-    Buf xq, sx, h, hq, sh, y, meta, tbl, rdesc;
+    Buf xq, sx, h, hq, sh, y, meta, tbl, rdesc, part_d, part_f;
     Buf pin_x, pin_y, pin_meta;
     hipEvent_t ev[N_EVENTS] = {};
     hipEvent_t phase_ev[4] = {};   // expert_group phases under profiling: H2D | kernels | D2H
@@ -95,6 +98,7 @@ struct Ctx {
     // no-allocation entry point), looked up at init with the device current
     uint8_t *fixed_scratch = nullptr;
     int *tail_ctr = nullptr;   // this device's copy of tail_ctr[]
+    int *split_ctr = nullptr;  // this device's copy of split_ctr[]
     // last device-resident table (for coli_hip_last_table)
     TableOut tbl_view{};
     int tbl_E = 0, tbl_R = 0;
@@ -238,14 +242,34 @@ int fused_route_mode() {
 // config 1, k = 1, 15.2 vs 18.2 us), 0 never, 1 whenever eligible.
 // COLI_HIP_FUSED_COMBINE=0 (1) in the environment sets 0 (1) at first use.
 std::atomic<int> g_fused_combine{-2};
-bool fused_combine_on(int k) {
+// Automatic mode leaves a split-K down projection (with its tail combine) in
+// place of the fused kernel.
+bool fused_combine_on(int k, bool down_split) {
     int m = g_fused_combine.load();
     if (m == -2) {
         const char *e = getenv("COLI_HIP_FUSED_COMBINE");
         m = e && e[0] == '0' ? 0 : (e && e[0] == '1' ? 1 : -1);
         g_fused_combine.store(m);
     }
-    return m == 1 || (m == -1 && k <= 2);
+    return m == 1 || (m == -1 && k <= 2 && !down_split);
+}
+
+// Split-K decode GEMV: the number of workgroups a GEMV launch aims for
+// (0: never split). COLI_HIP_GEMV_SPLIT in the environment sets it at first
+// use; coli_hip_set_gemv_split overrides it. Off by default: measured on
+// configs 1 and 2 the cross-workgroup hand-off (write-through pairs, the
+// device-scope counter, coherent reloads) costs more than the extra CUs
+// gain (config 1 gate/up 10.5 -> 11.4-14.4 us, down 5.4 -> 12.5-13.4 us;
+// config 2 gate/up 19.4 -> 33 us at five splits).
+constexpr int GEMV_SPLIT_DEFAULT = 0;
+std::atomic<int> g_gemv_split{-2};
+int gemv_split_target() {
+    int m = g_gemv_split.load();
+    if (m == -2) {
+        m = env_int("COLI_HIP_GEMV_SPLIT", GEMV_SPLIT_DEFAULT);
+        g_gemv_split.store(m);
+    }
+    return m < 0 ? GEMV_SPLIT_DEFAULT : m;
 }
 
 // COLI_HIP_TAIL_COMBINE=0 keeps the separate combine launch after a
@@ -293,6 +317,7 @@ int check_waits(Ctx *c) {
     // so a faulty dispatch cannot leave later ones a stale count
     if (c->tail_ctr) {
         hipMemsetAsync(c->tail_ctr, 0, GEMV_TAIL_TILES * sizeof(int), c->stream);
+        if (c->split_ctr) hipMemsetAsync(c->split_ctr, 0, GEMV_SPLIT_UNITS * sizeof(int), c->stream);
         hipStreamSynchronize(c->stream);
     }
     return fail("GEMV: a bounded wait between the streaming and chain waves gave up; the output of the "
@@ -409,7 +434,8 @@ int open_ctx(Ctx *c) {
                 "init: wait flag") ||
         !hip_ok(hipHostGetDevicePointer((void **)&c->wait_flag_dev, c->wait_flag, 0), "init: wait flag mapping") ||
         !hip_ok(hipGetSymbolAddress((void **)&c->fixed_scratch, HIP_SYMBOL(scratch)), "init: fixed scratch") ||
-        !hip_ok(hipGetSymbolAddress((void **)&c->tail_ctr, HIP_SYMBOL(tail_ctr)), "init: tail counters"))
+        !hip_ok(hipGetSymbolAddress((void **)&c->tail_ctr, HIP_SYMBOL(tail_ctr)), "init: tail counters") ||
+        !hip_ok(hipGetSymbolAddress((void **)&c->split_ctr, HIP_SYMBOL(split_ctr)), "init: split counters"))
         return 0;
     *c->wait_flag = 0;
     int lds = 0;
@@ -663,7 +689,40 @@ struct DispatchOpts {
     void *meta_dst = nullptr;
     int meta_n16 = 0;
     hipEvent_t after_quant = nullptr;   // recorded after the activation quantisation (profiling)
+    // split-K GEMV plans of the gate/up and down launches (split 0: unsplit)
+    // and their partial buffers (shared: the launches run one after the other)
+    GemvSplit split_gu, split_dn;
+    int32_t *part_d = nullptr;
+    float *part_f = nullptr;
+    int *split_ctr = nullptr;
 };
+
+// Plans the split-K GEMV launches of a dispatch with up to `rows` rows and
+// reserves their partial buffers (before any graph capture). The fused
+// router prologue and the per-block dot dump run only in the unsplit kernel.
+int plan_split(Ctx *c, const MatGeom &gg, const MatGeom &gd, int rows, int act, bool route_fused,
+               DispatchOpts *opt) {
+    const int target = gemv_split_target();
+    opt->split_gu = route_fused || g_dbg_gu ? GemvSplit{} : plan_gemv_split(gg, true, rows, act, target);
+    opt->split_dn = g_dbg_dn ? GemvSplit{} : plan_gemv_split(gd, false, rows, act, target);
+    const size_t bd = std::max(opt->split_gu.part_d_bytes, opt->split_dn.part_d_bytes);
+    const size_t bf = std::max(opt->split_gu.part_f_bytes, opt->split_dn.part_f_bytes);
+    if (!bd) return 1;
+    if (!reserve(c, c->part_d, bd) || (bf && !reserve(c, c->part_f, bf))) return 0;
+    opt->part_d = (int32_t *)c->part_d.p;
+    opt->part_f = (float *)c->part_f.p;
+    opt->split_ctr = c->split_ctr;
+    return 1;
+}
+
+void apply_split(DotArgs &d, const GemvSplit &p, const DispatchOpts &opt) {
+    d.split = p.split;
+    d.split_kb = p.kb;
+    d.split_nw = p.nw;
+    d.part_d = opt.part_d;
+    d.part_f = opt.part_f;
+    d.split_ctr = opt.split_ctr;
+}
 
 // The kernel sequence of one dispatch: quantise x (device memory, or mapped
 // host memory for the host-buffer calls), gate/up (+SwiGLU), [quantise h],
@@ -702,6 +761,7 @@ void run_experts(Ctx *c, Prof &prof, const ExpertDesc *desc, const RowPlan &plan
     da.spin_limit = g_spin_limit;
     da.wait_failed = c->wait_flag_dev;
     prof.mark(COLI_HIP_K_GATEUP);
+    if (arm == COLI_HIP_ARM_GEMV && !opt.route.logits) apply_split(da, opt.split_gu, opt);
     if (arm == COLI_HIP_ARM_GEMV)
         launch_gemv_gateup(da, gg, act, R_bound, c->stream);
     else
@@ -729,6 +789,7 @@ void run_experts(Ctx *c, Prof &prof, const ExpertDesc *desc, const RowPlan &plan
     dd.tail_out = opt.tail_out;
     dd.tail_w = opt.tail_w;
     dd.tail_ctr = opt.tail_ctr;
+    apply_split(dd, arm == COLI_HIP_ARM_GEMV ? opt.split_dn : GemvSplit{}, opt);
     prof.mark(COLI_HIP_K_DOWN);
     if (arm == COLI_HIP_ARM_GEMV && opt.combine_out) {
         launch_gemv_down_combine(dd, gd, act, opt.n_rows_fixed, opt.combine_w, opt.combine_out, c->stream);
@@ -766,7 +827,7 @@ bool graph_cache_enabled() {
 
 // A call's launch shape: fixed fields, then rows per expert (at most 256).
 // Built on the stack per call; a slot copies it only when a graph is stored.
-constexpr int SHAPE_FIELDS = 11, SHAPE_MAX = SHAPE_FIELDS + 256;
+constexpr int SHAPE_FIELDS = 12, SHAPE_MAX = SHAPE_FIELDS + 256;
 struct ShapeKey {
     int n = 0;
     int v[SHAPE_MAX];
@@ -939,6 +1000,7 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
     // eager, 79 -> 68.7 us from a cached graph (profiled, the copies alone had
     // taken 22 us in and 48 us out).
     DispatchOpts opt;
+    if (arm == COLI_HIP_ARM_GEMV && !plan_split(c, gg, gd, total, epi_act(ga), false, &opt)) return 0;
     opt.w_reuse = total >= 2 * MT_ROWS * count;   // about two or more M tiles per expert
     opt.meta_src = c->pin_meta.d;
     opt.meta_dst = dm;
@@ -981,7 +1043,8 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
     if (graphs_on && !profile && !g_dbg_gu && !g_dbg_dn) {
         const ColiHipTensor *g0 = gates[0], *d0 = downs[0];
         ShapeKey key;
-        shape_key(&key, {arm, count, D, gg.O, s_n, ga, g0->fmt, g0->gs, d0->fmt, d0->gs, g_spin_limit}, rows, count);
+        shape_key(&key, {arm, count, D, gg.O, s_n, ga, g0->fmt, g0->gs, d0->fmt, d0->gs, g_spin_limit, gemv_split_target()},
+                  rows, count);
         ColiHipGraph *g = graph_lookup(c, key);
         if (!g) {
             Prof off(c);
@@ -1320,6 +1383,12 @@ int coli_hip_set_fused_combine(int mode) {
     return 1;
 }
 
+int coli_hip_set_gemv_split(int target_wgs) {
+    if (target_wgs < -1) return fail("GEMV split target must be -1 (default), 0 (off) or a workgroup count");
+    g_gemv_split.store(target_wgs < 0 ? GEMV_SPLIT_DEFAULT : target_wgs);
+    return 1;
+}
+
 int coli_hip_set_fused_route(int mode) {
     if (mode < -1 || mode > 1) return fail("fused route mode must be -1, 0 or 1");
     g_fused_route.store(mode);
@@ -1517,8 +1586,12 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
     // fused router: worth it once the gate/up grid covers the chip (the
     // prologue costs every workgroup ~2 us; with few workgroups the separate
     // router launch, spread over many, is shorter)
+    // split-K GEMV (not on the no-allocation path: its partials would need
+    // more fixed scratch); a split gate/up has the router launched apart
     const int gu_wgs = k * ((gg.O + 31) / 32), fmode = fused_route_mode();
-    if (logits_dev && one_token && E <= ROUTE_MAX_E && (fmode == 1 || (fmode == -1 && gu_wgs >= 256))) {
+    const bool gemv_split = arm == COLI_HIP_ARM_GEMV && !fixed_scratch &&
+                            plan_gemv_split(gg, true, R, act, gemv_split_target()).split > 1;
+    if (logits_dev && one_token && E <= ROUTE_MAX_E && (fmode == 1 || (fmode == -1 && gu_wgs >= 256 && !gemv_split))) {
         // the gate/up GEMV routes and quantises the token itself
         opt.route = RouteArgs{logits_dev, E, k, ids_dev, w_dev, rdesc, x_dev, gg.K, gg.Kp, act};
         opt.x_quantized = true;
@@ -1530,7 +1603,9 @@ int moe_forward_impl(const ColiHipExpertSet *set, const float *x_dev, int S, con
     }
     // one token: the down GEMV also applies the router weights (one launch
     // fewer) when the k activation rows fit its LDS
-    const bool fuse_dc = one_token && fused_combine_on(k) && !g_dbg_dn && gemv_down_combine_ok(gd, k);
+    if (arm == COLI_HIP_ARM_GEMV && !fixed_scratch && !plan_split(c, gg, gd, R, act, opt.route.logits, &opt)) return 0;
+    const bool fuse_dc = one_token && fused_combine_on(k, opt.split_dn.split > 1) && !g_dbg_dn &&
+                         gemv_down_combine_ok(gd, k);
     if (fuse_dc) {
         opt.combine_w = w_dev;
         opt.combine_out = out_dev;

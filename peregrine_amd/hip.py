@@ -350,6 +350,13 @@ def set_fused_route(mode: int) -> None:
         raise HipError("coli_hip_set_fused_route failed")
 
 
+def set_gemv_split(target_wgs: int) -> None:
+    """Split-K decode GEMV: workgroups a GEMV launch aims for (0: never
+    split, -1: the default)."""
+    if lib.coli_hip_set_gemv_split(target_wgs) != 1:
+        raise HipError("coli_hip_set_gemv_split failed")
+
+
 def set_fused_combine(mode: int) -> None:
     """One token on the GEMV arm, down projection and combine in one launch:
     -1 automatic (k <= 2), 0 never, 1 whenever eligible (k <= 8, K <= 1536)."""
