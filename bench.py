@@ -141,6 +141,7 @@ def pcie_inclusive(hip, cfg, experts, x_step, ids, w, ga, seconds=0.5):
     out = {}
     for mode in ("eager", "graph_cache"):
         os.environ["COLI_HIP_GRAPH"] = "1" if mode == "graph_cache" else "0"
+        st0 = hip.graph_cache_stats()
         try:
             for _ in range(3):
                 hip.expert_group_reduce(sel, rows, xr, D, layout, rw, S)
@@ -152,6 +153,10 @@ def pcie_inclusive(hip, cfg, experts, x_step, ids, w, ga, seconds=0.5):
         finally:
             os.environ.pop("COLI_HIP_GRAPH", None)
         out[mode] = {"tokens_per_s": round(S / dt, 1), "ms_per_call": round(dt * 1e3, 4), "calls": n}
+        if mode == "graph_cache":   # the cache keeps replaying only where replay probed faster than eager
+            st1 = hip.graph_cache_stats()
+            out[mode]["replayed_calls"] = st1.replays - st0.replays
+            out[mode]["eager_calls"] = st1.uncacheable - st0.uncacheable
     out["entry_point"] = "coli_hip_expert_group_reduce (host x in, host out; blocking; Python ctypes call included)"
     return out
 
@@ -283,26 +288,26 @@ def run_workload(hip, cfg, wfmt, ga, arm, steps, warmup, use_graph=True, layers=
     n_all = warmup + steps
     bx = hip.DeviceBuffer(n_all * S * D * 4)
     bx.fill(n_all * S * D, 1, 0.0, 1.0, seed=7)
-    logits = make_logits(cfg, n_all, seed=11)
+    # router logits per step and layer: every layer is routed from its own
+    logits = make_logits(cfg, n_all * L, seed=11)
     if cfg["route"] == "one":
         logits[:] = 0.0
     bl = hip.DeviceBuffer.from_array(logits)
-    bids = hip.DeviceBuffer(n_all * S * k * 4)
-    bw = hip.DeviceBuffer(n_all * S * k * 4)
+    n_sel = n_all * L * S * k
+    bids = hip.DeviceBuffer(n_sel * 4)
+    bw = hip.DeviceBuffer(n_sel * 4)
     bh = [hip.DeviceBuffer(S * D * 4) for _ in range(2)]
     hip.pipe_sync(0)
     t_build = time.perf_counter() - t_build
 
     def step(i):
-        xp = bx.ptr + i * S * D * 4
-        ip, wp = bids.ptr + i * S * k * 4, bw.ptr + i * S * k * 4
-        cur = xp
+        cur = bx.ptr + i * S * D * 4
         for layer in range(L):
+            j = i * L + layer
+            ip, wp = bids.ptr + j * S * k * 4, bw.ptr + j * S * k * 4
             out = bh[layer & 1].ptr
-            if layer == 0:   # router fused with the first layer's activation quantisation
-                hip.moe_forward_logits_dev(layers[0][0], cur, S, bl.ptr + i * S * E * 4, k, ip, wp, out, ga, arm)
-            else:            # later resident layers reuse the step's routing
-                hip.moe_forward_dev(layers[layer][0], cur, S, ip, wp, k, out, ga, arm)
+            # device router (softmax top-k) fused with the layer's activation quantisation
+            hip.moe_forward_logits_dev(layers[layer][0], cur, S, bl.ptr + j * S * E * 4, k, ip, wp, out, ga, arm)
             cur = out
 
     # eager warm-up passes reserve all scratch (a graph must not allocate)
@@ -329,8 +334,9 @@ def run_workload(hip, cfg, wfmt, ga, arm, steps, warmup, use_graph=True, layers=
     ms_per_step = wall * 1e3 / steps
     del graph
 
-    # distinct experts each step touches (for algorithmic bytes)
-    ids = bids.download(np.int32, (n_all, S * k))[warmup:]
+    # distinct experts each layer of a step touches (for algorithmic bytes)
+    ids_all = bids.download(np.int32, (n_all * L, S * k))
+    ids = ids_all[warmup * L:]
     distinct = float(np.mean([len(np.unique(r)) for r in ids]))
 
     # profiled pass: per-kernel execution times from the dispatch packets
@@ -368,6 +374,8 @@ def run_workload(hip, cfg, wfmt, ga, arm, steps, warmup, use_graph=True, layers=
         "workload": wl_name,
         "value": round(S * L * steps / wall, 2),
         "unit": "tokens/s",
+        "value_unit": "MoE-layer tokens/s (tokens x layers per second)",
+        "stack_tokens_per_s": round(S * steps / wall, 2),
         "steps": steps,
         "warmup": warmup,
         "ms_per_step": round(ms_per_step, 4),
@@ -386,7 +394,7 @@ def run_workload(hip, cfg, wfmt, ga, arm, steps, warmup, use_graph=True, layers=
     if pcie and S <= 64 and L == 1:
         x0 = bx.download(np.float32, ((warmup + 1) * S, D))[warmup * S:]
         summary["pcie_inclusive"] = pcie_inclusive(hip, cfg, layers[0][1], x0, ids[0],
-                                                   bw.download(np.float32, (n_all, S * k))[warmup], ga)
+                                                   bw.download(np.float32, (n_all * L, S * k))[warmup * L], ga)
     for b in (bx, bl, bids, bw, *bh):
         b.free()
     return summary, layers
@@ -418,16 +426,25 @@ def main():
     # the headline configuration.
     wl = {}
     if not args.no_detail:
+        # every BASELINE configuration gets a driver-timed line with its own
+        # roofline: configs 1-4 int4, then config 5 with the other weight
+        # format than the headline's (configs 2-4 share one resident layer)
         shared = None
-        for cid in (2, 4):
-            if cid == args.config:
+        for cid, wf in ((1, "int4"), (2, "int4"), (3, "int4"), (4, "int4"),
+                        (5, "int8" if args.wfmt == "int4" else "int4")):
+            if (cid, wf) == (args.config, args.wfmt):
                 continue
             c2 = dict(CONFIGS[cid])
-            c2["seed"] = 2
+            c2["seed"] = cid if cid in (1, 5) else 2
             st = DEFAULT_STEPS[cid]
-            s, shared = run_workload(hip, c2, "int4", ga, -1, st, max(2, st // 10), layers=shared,
-                                     pcie=not args.no_pcie)
+            s, lay = run_workload(hip, c2, wf, ga, -1, st, max(2, st // 10),
+                                  layers=shared if cid in (2, 3, 4) else None, pcie=not args.no_pcie)
+            if cid in (2, 3, 4):
+                shared = lay
+            del lay
             wl[s["workload"]] = s
+            print(f"[bench] {s['workload']}: {s['value']} tokens/s, {s['ms_per_step']} ms/step, "
+                  f"roofline frac {s['roofline']['frac']}", file=sys.stderr, flush=True)
         del shared
     head, layers = run_workload(hip, cfg, args.wfmt, ga, arm, steps, warmup, use_graph=not args.no_graph,
                                 pcie=not args.no_pcie)
@@ -450,6 +467,9 @@ def main():
             "tokens": cfg["S"], "top_k": cfg["k"], "layers": cfg["layers"],
             "weights": f"{args.wfmt} QT, f32 scale per 32", "act_group": ga, "arm": args.arm,
             "graph": not args.no_graph, "parallelism": "none (1 GPU)",
+            "routing": "device softmax top-k per layer, from that layer's own router logits",
+            "value_unit": "MoE-layer tokens/s = tokens x layers per second",
+            "stack_tokens_per_s": head["stack_tokens_per_s"],
         },
         "roofline": head["roofline"],
         "detail": {k: v for k, v in head.items() if k not in ("value", "unit", "steps", "warmup", "ms_per_step",

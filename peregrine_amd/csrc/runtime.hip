@@ -10,6 +10,7 @@
 #include <cstring>
 #include <map>
 #include <atomic>
+#include <chrono>
 #include <mutex>
 #include <vector>
 
@@ -70,13 +71,23 @@ struct Buf {
 constexpr int GRAPH_CACHE = 16;   // cached expert-group graphs per device
 constexpr int N_EVENTS = 2 * (COLI_HIP_K_COUNT + 4);   // (start, stop) per kernel slot of a dispatch
 
-// One cached expert-group graph: its launch-shape key, the scratch generation
-// it was captured under and its last use (least recently used is evicted).
+// One launch shape of the expert-group graph cache: its key, its graph and
+// the scratch generation it was captured under, its last use (least recently
+// used is evicted), and whether replaying it pays. A new shape is captured,
+// then its next calls alternate replay and eager launch (GRAPH_PROBES of
+// each, timed on the host clock around enqueue and synchronise); the faster
+// one is kept. A shape where eager wins keeps no graph and runs eagerly.
+enum SlotState { SLOT_PROBE = 0, SLOT_GRAPH = 1, SLOT_EAGER = 2 };
+constexpr int GRAPH_PROBES = 3;
 struct GraphSlot {
+    bool live = false;
     uint64_t key = 0;
     ColiHipGraph *g = nullptr;
     unsigned gen = 0;
     uint64_t used = 0;
+    int state = SLOT_PROBE;
+    int n_graph = 0, n_eager = 0;
+    double t_graph = 0, t_eager = 0;   // fastest probe of each, seconds
 };
 
 struct Ctx {
@@ -820,9 +831,17 @@ struct ReduceSpec {
 // lookup (its baked addresses are stale); a failed capture drops them all.
 // ---------------------------------------------------------------------------
 bool graph_cache_enabled() {
+    // COLI_CUDA_GRAPH, the reference's knob, is read as an alias so that the
+    // unchanged Rust caller's environment keeps its meaning
     const char *v = std::getenv("COLI_HIP_GRAPH");
     if (!v || !*v) v = std::getenv("COLI_CUDA_GRAPH");
     return v && std::atoi(v) != 0;
+}
+
+// COLI_HIP_GRAPH_ADAPT=0: replay every cached shape, never decline one.
+bool graph_adapt() {
+    const char *v = std::getenv("COLI_HIP_GRAPH_ADAPT");
+    return !(v && v[0] == '0');
 }
 
 // A call's launch shape: fixed fields, then rows per expert (at most 256).
@@ -860,22 +879,25 @@ void drop_slot(GraphSlot &sl) {   // a graph whose baked scratch addresses are s
     g_graph_invalidations++;
 }
 
-ColiHipGraph *graph_lookup(Ctx *c, const ShapeKey &key) {
+// The shape's slot, or null. A slot whose graph was captured before a scratch
+// reallocation is dropped here (its baked addresses are stale), so the shape
+// is captured and probed again.
+GraphSlot *slot_lookup(Ctx *c, const ShapeKey &key) {
     const int ci = (int)(c - g_ctx);
     for (int i = 0; i < GRAPH_CACHE; i++) {
         GraphSlot &sl = c->graphs[i];
-        if (!sl.g || sl.key != key.hash || !slot_shape_is(g_slot_shape[ci][i], key)) continue;
-        if (sl.gen != c->gen) {   // scratch moved since the capture
+        if (!sl.live || sl.key != key.hash || !slot_shape_is(g_slot_shape[ci][i], key)) continue;
+        if (sl.g && sl.gen != c->gen) {
             drop_slot(sl);
             return nullptr;
         }
         sl.used = ++c->graph_clock;
-        return sl.g;
+        return &sl;
     }
     return nullptr;
 }
 
-void graph_store(Ctx *c, const ShapeKey &key, ColiHipGraph *g) {
+GraphSlot *graph_store(Ctx *c, const ShapeKey &key, ColiHipGraph *g) {
     const int ci = (int)(c - g_ctx);
     // graphs captured before a scratch reallocation can never replay: free
     // them (and their exec resources) before choosing an LRU victim
@@ -883,7 +905,7 @@ void graph_store(Ctx *c, const ShapeKey &key, ColiHipGraph *g) {
         if (c->graphs[i].g && c->graphs[i].gen != c->gen) drop_slot(c->graphs[i]);
     int victim = 0;
     for (int i = 0; i < GRAPH_CACHE; i++) {
-        if (!c->graphs[i].g) {
+        if (!c->graphs[i].live) {
             victim = i;
             break;
         }
@@ -891,11 +913,33 @@ void graph_store(Ctx *c, const ShapeKey &key, ColiHipGraph *g) {
     }
     GraphSlot &sl = c->graphs[victim];
     graph_destroy(sl.g);
+    sl = GraphSlot{};
+    sl.live = true;
     sl.key = key.hash;
     sl.g = g;
     sl.gen = c->gen;
     sl.used = ++c->graph_clock;
+    sl.state = graph_adapt() ? SLOT_PROBE : SLOT_GRAPH;
     g_slot_shape[ci][victim].assign(key.v, key.v + key.n);
+    return &sl;
+}
+
+// A probe's host time; once both ways have GRAPH_PROBES samples the faster
+// fastest sample wins (ties to the graph).
+void slot_probe(GraphSlot *sl, bool graph, double secs) {
+    if (graph) {
+        sl->t_graph = sl->n_graph++ ? std::min(sl->t_graph, secs) : secs;
+    } else {
+        sl->t_eager = sl->n_eager++ ? std::min(sl->t_eager, secs) : secs;
+    }
+    if (sl->n_graph < GRAPH_PROBES || sl->n_eager < GRAPH_PROBES) return;
+    if (sl->t_graph <= sl->t_eager) {
+        sl->state = SLOT_GRAPH;
+    } else {
+        sl->state = SLOT_EAGER;
+        graph_destroy(sl->g);
+        sl->g = nullptr;
+    }
 }
 
 int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, ColiHipTensor *const *downs,
@@ -1045,8 +1089,8 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
         ShapeKey key;
         shape_key(&key, {arm, count, D, gg.O, s_n, ga, g0->fmt, g0->gs, d0->fmt, d0->gs, g_spin_limit, gemv_split_target()},
                   rows, count);
-        ColiHipGraph *g = graph_lookup(c, key);
-        if (!g) {
+        GraphSlot *sl = slot_lookup(c, key);
+        if (!sl) {
             Prof off(c);
             off.on = false;
             int ok = hip_ok(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "graph begin capture");
@@ -1056,6 +1100,7 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
             hipGraphExec_t exec = nullptr;
             ok = ok && hip_ok(end, "graph end capture") &&
                  hip_ok(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "graph instantiate");
+            ColiHipGraph *g = nullptr;
             if (ok) g = (ColiHipGraph *)std::calloc(1, sizeof(ColiHipGraph));
             if (!g) {
                 // a failed capture: nothing recorded near it is trusted again
@@ -1069,16 +1114,36 @@ int expert_group_impl(ColiHipTensor *const *gates, ColiHipTensor *const *ups, Co
             g->exec = exec;
             g->device = device;
             g->gen = c->gen;
-            graph_store(c, key, g);
-            std::lock_guard<std::mutex> lock(g_stats_mu);
-            g_graph_captures++;
-        } else {
-            std::lock_guard<std::mutex> lock(g_stats_mu);
-            g_graph_replays++;
+            sl = graph_store(c, key, g);
+            {
+                std::lock_guard<std::mutex> lock(g_stats_mu);
+                g_graph_captures++;
+            }
+            if (!hip_ok(hipGraphLaunch(g->exec, c->stream), "expert group graph launch") ||
+                !hip_ok(hipStreamSynchronize(c->stream), "expert group graph synchronize"))
+                return 0;
+            return finish();
         }
-        if (!hip_ok(hipGraphLaunch(g->exec, c->stream), "expert group graph launch") ||
-            !hip_ok(hipStreamSynchronize(c->stream), "expert group graph synchronize"))
-            return 0;
+        // replay unless this shape runs eagerly (it lost its probes), or it
+        // is being probed and the eager side is behind
+        const bool replay = sl->state == SLOT_GRAPH || (sl->state == SLOT_PROBE && sl->n_graph <= sl->n_eager);
+        const auto t0 = std::chrono::steady_clock::now();
+        if (replay) {
+            if (!hip_ok(hipGraphLaunch(sl->g->exec, c->stream), "expert group graph launch") ||
+                !hip_ok(hipStreamSynchronize(c->stream), "expert group graph synchronize"))
+                return 0;
+        } else {
+            Prof off(c);
+            off.on = false;
+            if (!enqueue(off, false) || !hip_ok(hipStreamSynchronize(c->stream), "expert group synchronize")) return 0;
+        }
+        if (sl->state == SLOT_PROBE)
+            slot_probe(sl, replay, std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count());
+        {
+            std::lock_guard<std::mutex> lock(g_stats_mu);
+            if (replay) g_graph_replays++;
+            else g_graph_uncacheable++;   // ran eagerly with the cache on
+        }
         return finish();
     }
     if (graphs_on) {

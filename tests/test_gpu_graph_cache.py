@@ -136,6 +136,44 @@ def test_replayed_graph_uses_current_expert_weights(hip):
     assert after.replays >= before.replays + 1
 
 
+@pytest.mark.parametrize("adapt", [1, 0])
+def test_cache_probes_then_keeps_the_faster_way(hip, adapt):
+    """After its capture a shape's calls alternate replay and eager launch
+    (three timed probes each), then keep whichever was faster; a declined
+    shape runs eagerly and counts as uncacheable. With COLI_HIP_GRAPH_ADAPT=0
+    every call replays. Every call equals the eager result."""
+    say("graph cache adaptive", adapt)
+    D, I = 192, 96
+    ex = [_expert(hip, 0x9300 + i, D, I) for i in range(3)]
+    rows = [1, 2, 1 + adapt]   # a shape of its own per mode (a slot keeps its decision)
+    x = np.random.default_rng(0xADA).standard_normal((sum(rows), D)).astype(np.float32)
+    hip.set_act_group(32)
+    with graph_knob(False):
+        want = hip.expert_group(ex, rows, x, D)
+    old = os.environ.get("COLI_HIP_GRAPH_ADAPT")
+    os.environ["COLI_HIP_GRAPH_ADAPT"] = str(adapt)
+    try:
+        before = hip.graph_cache_stats()
+        with graph_knob(True):
+            for _ in range(12):
+                assert np.array_equal(want, hip.expert_group(ex, rows, x, D))
+        after = hip.graph_cache_stats()
+    finally:
+        if old is None:
+            os.environ.pop("COLI_HIP_GRAPH_ADAPT", None)
+        else:
+            os.environ["COLI_HIP_GRAPH_ADAPT"] = old
+    assert after.captures == before.captures + 1
+    replays = after.replays - before.replays
+    eager = after.uncacheable - before.uncacheable
+    assert replays + eager == 11
+    if adapt:
+        assert replays >= 3 and eager >= 3            # both ways were probed
+        assert replays in (3, 11 - 3)                 # then one way was kept for the remaining calls
+    else:
+        assert replays == 11 and eager == 0
+
+
 def test_profiled_calls_are_uncacheable_and_time_phases(hip):
     say("graph cache uncacheable + phase stats")
     D, I = 256, 128

@@ -609,6 +609,57 @@ def test_greedy_argmax_token_identical(hip, orc):
     assert np.array_equal(np.array(seq_g), np.array(seq_o))
 
 
+@pytest.mark.parametrize("ga,arm,B", [(32, -1, 1), (0, -1, 1), (32, 2, 4), (0, 0, 4), (32, -1, 64), (0, -1, 64)])
+def test_greedy_argmax_baseline_width(hip, orc, ga, arm, B):
+    """Greedy decoding at the BASELINE decode widths (generate_is_deterministic_greedy,
+    model.rs:5354-5366, restated on a MoE-only stack): D=5120, I=1536, two
+    MoE layers of 160 expert slots aliasing 12 distinct experts each, top-8
+    from the device router on host-computed router logits, residual, lm_head
+    argmax, 8 steps. Batch 1 runs the one-token decode path (automatic arm:
+    GEMV with the fused router), batch 4 forces each arm, batch 64 takes the
+    automatic MFMA arm. Every layer output and every generated token equals
+    the oracle's."""
+    say("greedy argmax baseline width", ga, arm, B)
+    rng = np.random.default_rng(0xC0FFEE + ga + B)
+    V, D, I, E, n_dist, k, L, steps = 96, 5120, 1536, 160, 12, 8, 2, 8
+    emb = rng.standard_normal((V, D)).astype(np.float32)
+    head = rng.standard_normal((V, D)).astype(np.float32)
+    layers = []
+    for _ in range(L):
+        gpu, ora = _experts(rng, n_dist, D, I, qt.FMT_I4G, 32, orc, hip)
+        router = (rng.standard_normal((E, D)) * 0.02).astype(np.float32)
+        layers.append((hip.ExpertSet([gpu[e % n_dist] for e in range(E)]), [ora[e % n_dist] for e in range(E)],
+                       router))
+    bx, bl = hip.DeviceBuffer(B * D * 4), hip.DeviceBuffer(B * E * 4)
+    bids, bw, bout = hip.DeviceBuffer(B * k * 4), hip.DeviceBuffer(B * k * 4), hip.DeviceBuffer(B * D * 4)
+    tok = rng.integers(0, V, B)
+    seq_g, seq_o = [], []
+    tok_g, tok_o = tok.copy(), tok.copy()
+    for step in range(steps):
+        xg, xo = emb[tok_g].copy(), emb[tok_o].copy()
+        for li, (eset, ora, router) in enumerate(layers):
+            lg = orc.matmul_f32(xg, router, D, E)
+            bx.upload(xg)
+            bl.upload(lg)
+            hip.moe_forward_logits_dev(eset, bx.ptr, B, bl.ptr, k, bids.ptr, bw.ptr, bout.ptr, ga, arm)
+            hip.pipe_sync(0)
+            og = bout.download(np.float32, (B, D))
+            lo = orc.matmul_f32(xo, router, D, E)
+            ids, w = orc.route_softmax_topk(lo, k)
+            oo = orc.moe_forward(xo, ids, w, ora, ga, nthreads=16, simd=orc.have_avx2())
+            assert np.array_equal(og, oo), (step, li, nerr(og, oo))
+            xg = (xg + og).astype(np.float32)
+            xo = (xo + oo).astype(np.float32)
+        tok_g = np.argmax(orc.matmul_f32(xg, head, D, V), axis=1)
+        tok_o = np.argmax(orc.matmul_f32(xo, head, D, V), axis=1)
+        seq_g.append(tok_g)
+        seq_o.append(tok_o)
+    assert np.array_equal(np.array(seq_g), np.array(seq_o))
+    # the stack is not degenerate: the batch's tokens differ
+    if B > 1:
+        assert len(np.unique(np.array(seq_g))) > 1
+
+
 @pytest.mark.parametrize("arm", [-1, 0, 2])
 def test_golden_layer_bit_exact(hip, arm):
     """The committed fixture (tests/golden/moe_layer_small.npz): device
