@@ -93,14 +93,17 @@ int coli_hip_expert_group_reduce(ColiHipTensor *const *gates, ColiHipTensor *con
                                  const float *x);                 /* coli_cuda_expert_group_reduce */
 
 /* ---- graphs: replaces backend_cuda.h:172-190 ----
- * With COLI_HIP_GRAPH=1 (or the reference's COLI_CUDA_GRAPH=1) in the
- * environment, expert_group* calls are captured once per launch shape (arm,
- * expert count, widths, rows per expert, reduce rows, formats) and replayed;
- * descriptors and activations reach the graph through mapped host staging
- * that the replayed kernels read (and the output is written back the same
- * way), so a replay uses the current experts and inputs. Not cached:
- * calls under profiling or with the debug-dot hook set (graph_cache_stats
- * counts them as uncacheable). */
+ * With COLI_HIP_GRAPH=1 in the environment (COLI_CUDA_GRAPH=1, the
+ * reference's name, is read as an alias), expert_group* calls are captured
+ * once per launch shape (arm, expert count, widths, rows per expert, reduce
+ * rows, formats) and replayed; descriptors and activations reach the graph
+ * through mapped host staging that the replayed kernels read (and the output
+ * is written back the same way), so a replay uses the current experts and
+ * inputs. A new shape's next calls alternate replay and eager launch (three
+ * timed probes each) and the faster is kept; a shape where eager wins runs
+ * eagerly from then on (COLI_HIP_GRAPH_ADAPT=0 always replays). Not cached:
+ * calls under profiling or with the debug-dot hook set. graph_cache_stats
+ * counts every call that ran eagerly with the cache on as uncacheable. */
 int coli_hip_graph_begin(int device);                             /* coli_cuda_graph_begin */
 int coli_hip_graph_end(int device, ColiHipGraph **out);           /* coli_cuda_graph_end */
 /* graph_launch refuses (returns 0) a graph captured before the device's

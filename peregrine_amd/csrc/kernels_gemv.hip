@@ -93,6 +93,10 @@ __device__ __forceinline__ void spin_until_geq(int *ctr, int target, int limit, 
 // (write-through / coherent reads of just those lines), the stores have
 // completed (vmcnt 0) before the count is incremented, the count is an
 // agent-scope read-modify-write, and the loads issue only after it returns.
+// This rests on the code gfx942/gfx950 get for agent-scope relaxed atomics
+// (stores and loads with the SC1 cache policy: written through to, and read
+// from, the device coherence point), not on a language-level release/acquire
+// pair, whose whole-L2 write-back and invalidate is what the scheme avoids.
 __device__ __forceinline__ void tail_combine(const DotArgs &a, int O, int nrows, int o, int tile) {
     const int lane = threadIdx.x & 63;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
