@@ -279,14 +279,18 @@ def measured_traffic(workload):
         lines = open(TRAFFIC_FILE).read().splitlines()
     except OSError:
         return None
+    col = None
     for ln in lines:
         cells = [c.strip() for c in ln.strip().strip("|").split("|")]
-        if len(cells) < 3 or cells[0] != workload or "<" not in cells[1]:
+        if "traffic B" in cells:   # the table's header names the column
+            col = cells.index("traffic B")
+            continue
+        if col is None or len(cells) <= col or cells[0] != workload or "<" not in cells[1]:
             continue
         targs = [t.strip() for t in cells[1].split("<", 1)[1].rstrip(">").split(",")]
         if len(targs) >= 3 and targs[2] == "true":   # the gate/up instantiation
             try:
-                return int(float(cells[-1]))
+                return int(float(cells[col]))
             except ValueError:
                 return None
     return None

@@ -11,7 +11,7 @@ sys.path.insert(0, ROOT)
 import bench  # noqa: E402
 
 
-@pytest.mark.parametrize("cfg_id,wfmt", [(2, "int4"), (3, "int4"), (4, "int4"), (5, "int4"), (5, "int8")])
+@pytest.mark.parametrize("cfg_id,wfmt", [(1, "int4"), (2, "int4"), (3, "int4"), (4, "int4"), (5, "int4"), (5, "int8")])
 def test_traffic_for_every_bench_workload(cfg_id, wfmt):
     cfg = dict(bench.CONFIGS[cfg_id])
     name = cfg["name"] + ("_int8" if wfmt == "int8" else "")
@@ -19,7 +19,9 @@ def test_traffic_for_every_bench_workload(cfg_id, wfmt):
     assert isinstance(t, int)
     # at least the algorithmic bytes of the fewest distinct experts a step can touch
     gu_one, _, _, _ = bench.algorithmic(cfg, wfmt, 1)
-    assert t >= cfg["k"] * gu_one * 0.99
+    assert t >= min(cfg["k"], cfg["E"]) * gu_one * 0.99
+    # and not absurdly above what every expert of the layer would read twice
+    assert t <= 2 * cfg["E"] * gu_one
 
 
 def test_traffic_unknown_workload_is_none():
