@@ -36,7 +36,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
 INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA, published (no sparsity)
 
-# BASELINE.json configs, numbered 1..5 as in BASELINE.md
+# The five benchmark configurations, numbered 1..5
 CONFIGS = {
     1: dict(name="cfg1_single_expert_1tok", E=1, D=5120, I=1536, S=1, k=1, route="one", layers=1),
     2: dict(name="cfg2_decode_moe_layer_b1_160x_int4", E=160, D=5120, I=1536, S=1, k=8, route="normal", layers=1),
@@ -164,10 +164,11 @@ def pcie_inclusive(hip, cfg, experts, x_step, ids, w, ga, seconds=0.5):
                     call(*args)
                 n += 50
             dt = (time.perf_counter() - t0) / n
-            assert np.array_equal(res, ref), "host-buffer call disagrees with its first result"
+            same = bool(np.array_equal(res, ref))
         finally:
             os.environ.pop("COLI_HIP_GRAPH", None)
-        out[mode] = {"tokens_per_s": round(S / dt, 1), "ms_per_call": round(dt * 1e3, 4), "calls": n}
+        out[mode] = {"tokens_per_s": round(S / dt, 1), "ms_per_call": round(dt * 1e3, 4), "calls": n,
+                     "equals_python_mirror_call": same}
         if mode == "graph_cache":   # the cache keeps replaying only where replay probed faster than eager
             st1 = hip.graph_cache_stats()
             out[mode]["replayed_calls"] = st1.replays - st0.replays
